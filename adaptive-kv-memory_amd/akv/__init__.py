@@ -1,0 +1,33 @@
+"""akv -- MI355X-native warm-tier hot path of Adaptive KV Memory.
+
+Module paths, names and signatures follow the reference package
+(akv/__init__.py:47-63 re-exports the fused ops); every op runs hand-written
+gfx950 kernels from libakv_hip.so.
+"""
+from .affine_quantizer import AffineQuantConfig, AffineQuantizer
+from .bitpack import pack, unpack, packed_bytes
+from .drop_in import AKVCache, _PRESETS, select_demote_indices
+from .fused_attention import fused_int4_decode_attention, mixed_precision_decode_attention
+from .importance import ImportanceConfig, ImportanceScorer, ScoringStrategy
+from .quantizer import KVQuantizer, QuantConfig, QuantizedTensor
+from .triton_kernels import fused_decode_attention, fused_quantize_evict
+from .triton_ops import (
+    HAS_TRITON,
+    fused_importance_update,
+    fused_mixed_precision_attention,
+    fused_quantized_attention,
+)
+from .warm_tier import WarmTier, decode_attention, dequantize, quantize_kv
+
+__version__ = "0.1.0"
+
+__all__ = [
+    "AffineQuantConfig", "AffineQuantizer", "pack", "unpack", "packed_bytes",
+    "AKVCache", "_PRESETS", "select_demote_indices",
+    "fused_int4_decode_attention", "mixed_precision_decode_attention",
+    "ImportanceConfig", "ImportanceScorer", "ScoringStrategy",
+    "KVQuantizer", "QuantConfig", "QuantizedTensor",
+    "fused_decode_attention", "fused_quantize_evict",
+    "HAS_TRITON", "fused_importance_update", "fused_mixed_precision_attention", "fused_quantized_attention",
+    "WarmTier", "decode_attention", "dequantize", "quantize_kv",
+]

@@ -1,0 +1,131 @@
+"""AKVCache presets and the demotion primitives of the drop-in cache.
+
+``_PRESETS`` and the preset resolution of ``AKVCache.__init__`` follow
+akv/drop_in.py:89-124 and :910-964.  Demotion follows ``AKVLayer``:
+``select_demote_indices`` is akv/drop_in.py:392-413 (first 4 and last
+min(16, hot_budget // 4) hot tokens protected, lowest scores first, indices
+returned in ascending order) and ``demote`` gathers the selected tokens and
+quantizes them into the packed warm tier on the device (the reference's
+_quantize_per_head at akv/drop_in.py:315-374 quantizes and immediately
+dequantizes back to fp16; here the packed codes are what is kept).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _native as nat
+from .warm_tier import WarmTier, quantize_kv
+
+_PRESETS = {
+    "quality": {
+        "warm_bits": 4,
+        "hot_budget": 256,
+        "description": "Near-lossless 4-bit. +1-2% PPL.",
+    },
+    "balanced": {
+        "warm_bits": 3,
+        "hot_budget": 128,
+        "description": "Block-affine 3-bit. +3.3% PPL, 5x compression.",
+    },
+    "compact": {
+        "warm_bits": 2,
+        "hot_budget": 64,
+        "description": "Block-affine 2-bit. +11% PPL, 8x compression.",
+    },
+    "k4v2": {
+        "warm_bits": 4,
+        "warm_key_bits": 4,
+        "warm_value_bits": 2,
+        "hot_budget": 128,
+        "description": "Asymmetric K4/V2. Keys preserved, values aggressively compressed.",
+    },
+    "k4v3": {
+        "warm_bits": 4,
+        "warm_key_bits": 4,
+        "warm_value_bits": 3,
+        "hot_budget": 128,
+        "description": "Asymmetric K4/V3. Near-quality keys with balanced value compression.",
+    },
+}
+
+
+def select_demote_indices(importance: Optional[torch.Tensor], n_demote: int, hot_len: int,
+                          hot_budget: int) -> torch.Tensor:
+    """akv/drop_in.py:392-413 on the device (importance (hot_len,) or (B, hot_len))."""
+    if importance is None or importance.shape[-1] != hot_len:
+        dev = importance.device if importance is not None else None
+        return torch.arange(n_demote, device=dev)
+    nat.require_device(importance)
+    protect_initial = 4
+    protect_recent = min(16, hot_budget // 4)
+    scores = importance.to(torch.float32).clone()
+    scores[..., :protect_initial] = float("inf")
+    scores[..., max(0, hot_len - protect_recent):] = float("inf")
+    _, idx = scores.topk(n_demote, dim=-1, largest=False)
+    idx, _ = idx.sort(dim=-1)
+    return idx
+
+
+class AKVCache:
+    """Preset resolution and warm-tier settings of the drop-in cache
+    (akv/drop_in.py:885-964).  The HF ``DynamicCache`` wiring is not part of
+    this build; ``demote`` is the warm-tier hot path it drives."""
+
+    def __init__(self, preset: Optional[str] = None, warm_bits: Optional[int] = None,
+                 warm_key_bits: Optional[int] = None, warm_value_bits: Optional[int] = None,
+                 hot_budget: Optional[int] = None, group_size: int = 64, outlier_fraction: float = 0.0,
+                 protect_first: int = 0, protect_last: int = 0, protect_layers: Optional[list] = None,
+                 num_hidden_layers: Optional[int] = None, enable_promotion: bool = True,
+                 promotion_threshold: float = 0.05, enable_promotion_proxy: bool = True,
+                 proxy_decay: float = 0.7, adaptive_hot_frac: float = 0.0,
+                 block_t: int = 32, group_v: int = 32):
+        if preset is not None:
+            if preset not in _PRESETS:
+                raise ValueError(f"Unknown preset {preset!r}. Choose from: {sorted(_PRESETS.keys())}")
+            if warm_bits is not None or hot_budget is not None:
+                raise ValueError(
+                    "preset= is mutually exclusive with warm_bits/hot_budget. "
+                    "Pick a preset OR pass explicit params.")
+            p = _PRESETS[preset]
+            self.warm_bits = p["warm_bits"]
+            self.hot_budget = p["hot_budget"]
+        else:
+            self.warm_bits = warm_bits or 3
+            self.hot_budget = hot_budget or 128
+        if preset and "warm_key_bits" in _PRESETS.get(preset, {}):
+            self.warm_key_bits = _PRESETS[preset]["warm_key_bits"]
+            self.warm_value_bits = _PRESETS[preset]["warm_value_bits"]
+        else:
+            self.warm_key_bits = warm_key_bits or self.warm_bits
+            self.warm_value_bits = warm_value_bits or self.warm_bits
+        self.preset = preset
+        self.group_size = group_size
+        self.outlier_fraction = outlier_fraction
+        self.num_hidden_layers = num_hidden_layers
+        self.enable_promotion = enable_promotion
+        self.promotion_threshold = promotion_threshold
+        self.enable_promotion_proxy = enable_promotion_proxy
+        self.proxy_decay = proxy_decay
+        self.adaptive_hot_frac = adaptive_hot_frac
+        self._protect_first = protect_first
+        self._protect_last = protect_last
+        self._protect_explicit = list(protect_layers) if protect_layers else []
+        self.block_t = block_t
+        self.group_v = group_v
+
+    def demote(self, keys: torch.Tensor, values: torch.Tensor, importance: Optional[torch.Tensor],
+               n_demote: int) -> tuple[WarmTier, torch.Tensor]:
+        """Pick ``n_demote`` hot tokens per sequence (lowest importance, protected
+        ends kept) and quantize them into a packed warm tier.
+
+        keys / values: (B, H, hot_len, D) on the device; importance: (B, hot_len)
+        or (hot_len,).  Returns (warm tier, selected indices (B, n_demote))."""
+        B, H, hot_len, D = keys.shape
+        idx = select_demote_indices(importance, n_demote, hot_len, self.hot_budget)
+        if idx.dim() == 1:
+            idx = idx.unsqueeze(0).expand(B, -1)
+        warm = quantize_kv(keys, values, self.warm_key_bits, self.warm_value_bits, self.block_t,
+                           self.group_v, self.outlier_fraction, sel=idx)
+        return warm, idx

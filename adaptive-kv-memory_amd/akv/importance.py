@@ -1,0 +1,120 @@
+"""ImportanceScorer accumulate rule on the device (akv/importance.py:19-164).
+
+The attention-sum strategies (ATTENTION_ACCUMULATION, IMPORTANCE) update a
+per-layer fp32 score vector with
+    scores[:N] = scores[:N] * decay + sum_q mean_{b,h} attn[b, h, q, :]
+through ``akv_importance_update``; the score vector grows with zeros when the
+context grows (akv/importance.py:100-108).  Strategies that are not the
+attention-sum rule are policy outside this hot path and raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+from dataclasses import dataclass
+from enum import Enum
+from typing import Optional
+
+import torch
+
+from . import _native as nat
+
+logger = logging.getLogger(__name__)
+
+
+class ScoringStrategy(str, Enum):
+    ATTENTION_ACCUMULATION = "attention_accumulation"
+    HEAVY_HITTER = "heavy_hitter"
+    RECENCY_WEIGHTED = "recency_weighted"
+    HYBRID = "hybrid"
+    IMPORTANCE = "importance"
+    FIFO = "fifo"
+    OBSERVATION_WINDOW = "observation_window"
+
+
+@dataclass
+class ImportanceConfig:
+    """akv/importance.py:30-43."""
+    strategy: ScoringStrategy = ScoringStrategy.HYBRID
+    decay_factor: float = 0.95
+    recency_weight: float = 0.3
+    attention_weight: float = 0.7
+    window_size: int = 64
+    initial_tokens_protected: int = 4
+    recent_tokens_protected: int = 32
+    observation_window: int = 32
+    pooling_kernel: int = 7
+
+
+_ACCUMULATE = (ScoringStrategy.ATTENTION_ACCUMULATION, ScoringStrategy.IMPORTANCE)
+
+
+def accumulate(scores: torch.Tensor, attention_weights: torch.Tensor, decay: float) -> torch.Tensor:
+    """scores (n,) fp32 on the device, in place: scores = scores*decay + sum_q mean_{b,h} attn
+    (truncated / zero-padded to n)."""
+    nat.require_device(scores, attention_weights)
+    lib = nat.load()
+    B, H, M, N = attention_weights.shape
+    attn = attention_weights
+    if attn.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        attn = attn.float()
+    attn = nat.dev_contig(attn)
+    a = nat.ImportanceArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.attn_dtype = nat.dtype_code(attn.dtype)
+    a.attn = attn.data_ptr()
+    a.B, a.H, a.M, a.N = B, H, M, N
+    a.scores = scores.data_ptr()
+    a.n_scores = scores.numel()
+    a.decay = float(decay)
+    nat.check(lib.akv_importance_update(ctypes.byref(a), nat.stream_of(scores)), "importance update")
+    return scores
+
+
+class ImportanceScorer:
+    """Per-layer running importance scores (akv/importance.py:46-164)."""
+
+    def __init__(self, config: Optional[ImportanceConfig] = None):
+        self.config = config or ImportanceConfig()
+        self._scores: dict[int, torch.Tensor] = {}
+        self._step_count: int = 0
+        self._total_seq_len: int = 0
+
+    def reset(self):
+        self._scores.clear()
+        self._step_count = 0
+        self._total_seq_len = 0
+
+    @property
+    def step_count(self) -> int:
+        return self._step_count
+
+    def update(self, attention_weights: Optional[torch.Tensor], layer_idx: int):
+        if attention_weights is None:
+            return
+        cfg = self.config
+        if cfg.strategy not in _ACCUMULATE:
+            raise NotImplementedError(f"strategy {cfg.strategy} is outside the attention-sum hot path")
+        kv_len = attention_weights.shape[-1]
+        device = attention_weights.device
+        old = self._scores.get(layer_idx)
+        if old is None or old.shape[0] < kv_len:
+            new = torch.zeros(kv_len, dtype=torch.float32, device=device)
+            if old is not None:
+                new[: old.shape[0]] = old.to(device)
+            self._scores[layer_idx] = new
+        scores = self._scores[layer_idx]
+        # only the first kv_len entries take the EMA (akv/importance.py:127-128)
+        accumulate(scores[:kv_len] if scores.shape[0] > kv_len else scores, attention_weights, cfg.decay_factor)
+        self._total_seq_len = max(self._total_seq_len, kv_len)
+        self._step_count += 1
+
+    def get_scores(self, layer_idx: int) -> Optional[torch.Tensor]:
+        return self._scores.get(layer_idx)
+
+    def stats(self) -> dict:
+        return {
+            "num_layers_tracked": len(self._scores),
+            "step_count": self._step_count,
+            "total_seq_len": self._total_seq_len,
+        }

@@ -1,0 +1,387 @@
+// extern "C" entry points of libakv_hip.so: argument validation, split
+// planning, workspace carving and dispatch to the kernels.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "akv_common.h"
+#include "decode.h"
+#include "misc.h"
+#include "quant.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+int ok() {
+    g_err.clear();
+    return AKV_OK;
+}
+int hip_fail(hipError_t e, const char *what) {
+    return fail(AKV_E_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+bool pow2(int x) { return x > 0 && (x & (x - 1)) == 0; }
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+int64_t align256(int64_t x) { return round_up(x, 256); }
+
+struct Plan {
+    int nchunk, prows, n_wsplit, n_hsplit, nsplit;
+    int64_t wsplit_len, hsplit_len, N;
+    int64_t part_bytes, rowstat_bytes, flag_bytes, stash_bytes, total;
+};
+
+constexpr int kWaves = 4;
+
+// Deterministic split schedule: about `target` splits per (batch, kv-head,
+// row chunk), each a multiple of the K meta unit (warm) or 16 tokens (hot),
+// and at least one unit per wave.
+void make_plan(const akv_decode_args *a, Plan *pl) {
+    const akv_warm_desc &w = a->warm;
+    const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
+    const int64_t nh = a->n_hot;
+    const int g = a->Hq / a->Hkv;
+    const int R = g * a->M;
+    pl->nchunk = (R + 15) / 16;
+    pl->prows = R < 16 ? R : 16;
+    pl->N = nw + nh;
+    const int64_t pairs = (int64_t)a->B * a->Hkv * pl->nchunk;
+    int64_t target = a->num_splits > 0 ? a->num_splits : (1024 + pairs - 1) / pairs;
+    if (target < 1) target = 1;
+    const int64_t unit = (w.kind == AKV_WARM_AFFINE) ? w.block_t : 16;
+    int64_t len = (pl->N + target - 1) / target;
+    if (len < 1) len = 1;
+    pl->wsplit_len = round_up(len > kWaves * unit ? len : kWaves * unit, unit);
+    pl->hsplit_len = round_up(len > kWaves * 16 ? len : kWaves * 16, 16);
+    pl->n_wsplit = nw > 0 ? (int)((nw + pl->wsplit_len - 1) / pl->wsplit_len) : 0;
+    pl->n_hsplit = nh > 0 ? (int)((nh + pl->hsplit_len - 1) / pl->hsplit_len) : 0;
+    pl->nsplit = pl->n_wsplit + pl->n_hsplit;
+    pl->part_bytes = align256(pairs * pl->nsplit * (int64_t)pl->prows * (a->D + 2) * 4);
+    pl->rowstat_bytes = align256((int64_t)a->B * a->Hq * a->M * 2 * 4);
+    pl->flag_bytes = 256;
+    const bool need_stash = a->attn_weights == nullptr && a->scores != nullptr;
+    pl->stash_bytes = need_stash ? align256((int64_t)a->B * a->Hq * a->M * pl->N * 4) : 0;
+    pl->total = pl->part_bytes + pl->rowstat_bytes + pl->flag_bytes + pl->stash_bytes;
+}
+
+int check_decode(const akv_decode_args *a) {
+    if (!a) return fail(AKV_E_INVALID, "args is NULL");
+    if (a->abi_version != AKV_ABI_VERSION)
+        return fail(AKV_E_ABI, "args built for ABI %d, library is ABI %d", a->abi_version, AKV_ABI_VERSION);
+    if (a->q_dtype != AKV_DT_F16) return fail(AKV_E_DTYPE, "decode attention takes float16 queries");
+    if (a->D != 64 && a->D != 128) return fail(AKV_E_SHAPE, "head_dim %d unsupported (64 or 128)", a->D);
+    if (a->B < 1 || a->Hq < 1 || a->Hkv < 1 || a->M < 1)
+        return fail(AKV_E_SHAPE, "B, Hq, Hkv, M must be >= 1");
+    if (a->Hq % a->Hkv) return fail(AKV_E_SHAPE, "Hq (%d) must be a multiple of Hkv (%d)", a->Hq, a->Hkv);
+    if (a->n_hot < 0) return fail(AKV_E_SHAPE, "n_hot < 0");
+    const akv_warm_desc &w = a->warm;
+    const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
+    if (nw < 0) return fail(AKV_E_SHAPE, "n_warm < 0");
+    if (a->n_hot + nw < 1) return fail(AKV_E_SHAPE, "no tokens to attend to");
+    if (!a->q || !a->out) return fail(AKV_E_INVALID, "q and out are required");
+    if (!aligned16(a->q) || !aligned16(a->out)) return fail(AKV_E_ALIGN, "q/out must be 16-byte aligned");
+    if (a->n_hot > 0) {
+        if (!a->k_hot || !a->v_hot) return fail(AKV_E_INVALID, "k_hot/v_hot required when n_hot > 0");
+        if (!aligned16(a->k_hot) || !aligned16(a->v_hot)) return fail(AKV_E_ALIGN, "hot tier must be 16-byte aligned");
+        if (a->n_hot * a->D * 2 >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "hot tier per head exceeds 4 GiB");
+    }
+    if (w.kind == AKV_WARM_AFFINE) {
+        for (int bits : {w.bits_k, w.bits_v})
+            if (bits < 2 || bits > 4) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
+        if (w.block_t < 16 || w.block_t % 16) return fail(AKV_E_SHAPE, "block_t must be a positive multiple of 16");
+        if (w.group_v < 8 || w.group_v % 8 || a->D % w.group_v)
+            return fail(AKV_E_SHAPE, "group_v must be a multiple of 8 dividing D");
+        if (!w.k_codes || !w.v_codes || !w.k_scale || !w.k_zero || !w.v_scale || !w.v_zero)
+            return fail(AKV_E_INVALID, "warm tier pointers missing");
+        if (w.n_out < 0 || w.n_out > a->D) return fail(AKV_E_SHAPE, "n_out out of range");
+        if (w.n_out > 0 && (!w.k_oidx || !w.v_oidx || !w.k_odata || !w.v_odata))
+            return fail(AKV_E_INVALID, "outlier pointers missing");
+        if (nw * (int64_t)a->D >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "warm tier per head exceeds 4 GiB");
+    } else if (w.kind == AKV_WARM_LEGACY) {
+        if (w.bits_k != w.bits_v) return fail(AKV_E_BITS, "legacy warm tier uses one width for K and V");
+        if (w.bits_k != 2 && w.bits_k != 4 && w.bits_k != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", w.bits_k);
+        if (!pow2(w.group_size) || w.group_size < 8) return fail(AKV_E_UNSUPPORTED, "group_size must be a power of two >= 8");
+        if (w.meta_dtype < 0 || w.meta_dtype > 2) return fail(AKV_E_DTYPE, "bad meta dtype");
+        if (w.warm_heads != 1 && w.warm_heads != a->Hkv) return fail(AKV_E_SHAPE, "warm_heads must be 1 or Hkv");
+        if (!w.k_codes || !w.v_codes || !w.k_scale || !w.k_zero || !w.v_scale || !w.v_zero)
+            return fail(AKV_E_INVALID, "warm tier pointers missing");
+        if (nw * (int64_t)a->D * 2 >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "warm tier per head exceeds 4 GiB");
+    } else if (w.kind != AKV_WARM_NONE) {
+        return fail(AKV_E_INVALID, "unknown warm kind %d", w.kind);
+    }
+    if (w.kind != AKV_WARM_NONE && nw > 0) {
+        if (!aligned16(w.k_codes) || !aligned16(w.v_codes) || !aligned16(w.k_scale) || !aligned16(w.v_scale) ||
+            !aligned16(w.k_zero) || !aligned16(w.v_zero))
+            return fail(AKV_E_ALIGN, "warm tier must be 16-byte aligned");
+    }
+    if (a->scores && a->n_scores < 0) return fail(AKV_E_SHAPE, "n_scores < 0");
+    return AKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int akv_abi_version(void) { return AKV_ABI_VERSION; }
+const char *akv_last_error(void) { return g_err.c_str(); }
+
+int64_t akv_struct_size(int32_t which) {
+    switch (which) {
+        case 0: return (int64_t)sizeof(akv_warm_desc);
+        case 1: return (int64_t)sizeof(akv_decode_args);
+        case 2: return (int64_t)sizeof(akv_quant_args);
+        case 3: return (int64_t)sizeof(akv_dequant_args);
+        case 4: return (int64_t)sizeof(akv_importance_args);
+        default: return -1;
+    }
+}
+
+int64_t akv_decode_workspace_bytes(const akv_decode_args *a) {
+    if (check_decode(a) != AKV_OK) return -1;
+    Plan pl;
+    make_plan(a, &pl);
+    return pl.total;
+}
+
+int akv_decode_attn(const akv_decode_args *a, void *stream) {
+    int rc = check_decode(a);
+    if (rc != AKV_OK) return rc;
+    Plan pl;
+    make_plan(a, &pl);
+    if (!a->workspace || a->workspace_bytes < pl.total)
+        return fail(AKV_E_WORKSPACE, "workspace of %lld bytes needed", (long long)pl.total);
+    if (!aligned16(a->workspace)) return fail(AKV_E_ALIGN, "workspace must be 16-byte aligned");
+    const akv_warm_desc &w = a->warm;
+    akv::DecodeParams p{};
+    p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.M = a->M; p.D = a->D;
+    p.g = a->Hq / a->Hkv; p.R = p.g * a->M; p.nchunk = pl.nchunk; p.prows = pl.prows;
+    p.q = (const _Float16 *)a->q;
+    p.khot = (const _Float16 *)a->k_hot; p.vhot = (const _Float16 *)a->v_hot;
+    p.n_hot = a->n_hot;
+    const int wk = w.kind == AKV_WARM_NONE ? AKV_WARM_AFFINE : w.kind;
+    p.n_warm = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
+    int kb = 4, vb = 4;
+    int sym_src[2] = {0, 0};
+    const int *sym_ptr = nullptr;
+    char *ws = (char *)a->workspace;
+    p.part = (float *)ws;
+    p.rowstats = (float *)(ws + pl.part_bytes);
+    int *flags = (int *)(ws + pl.part_bytes + pl.rowstat_bytes);
+    float *stash_ws = (float *)(ws + pl.part_bytes + pl.rowstat_bytes + pl.flag_bytes);
+    if (w.kind == AKV_WARM_AFFINE) {
+        kb = w.bits_k; vb = w.bits_v;
+        p.kc = w.k_codes; p.vc = w.v_codes;
+        p.ks = w.k_scale; p.kz = w.k_zero; p.vs = w.v_scale; p.vz = w.v_zero;
+        p.kc_row = a->D * kb / 8; p.vc_row = a->D * vb / 8;
+        p.T = w.block_t; p.Gv = w.group_v;
+        p.nblk = (p.n_warm + w.block_t - 1) / w.block_t;
+        p.n_out = w.n_out;
+        p.k_oidx = w.k_oidx; p.v_oidx = w.v_oidx;
+        p.k_odata = (const _Float16 *)w.k_odata; p.v_odata = (const _Float16 *)w.v_odata;
+        p.warm_heads = a->Hkv;
+    } else if (w.kind == AKV_WARM_LEGACY) {
+        kb = vb = w.bits_k;
+        const int pD = (int)round_up(a->D, w.group_size);
+        p.kc = w.k_codes; p.vc = w.v_codes;
+        p.ks = w.k_scale; p.kz = w.k_zero; p.vs = w.v_scale; p.vz = w.v_zero;
+        p.kc_row = p.vc_row = pD * kb / 8;
+        p.gs = w.group_size; p.lg = pD / w.group_size; p.meta_dt = w.meta_dtype;
+        p.warm_heads = w.warm_heads;
+        p.half_max_k = p.half_max_v = (float)(((1 << kb) - 1) / 2);
+        p.T = 16;
+        if (w.legacy_sym < 0) {
+            p.sym_flags = flags;
+            sym_src[0] = w.meta_dtype;
+            sym_src[1] = (int)((int64_t)w.warm_heads * p.n_warm * p.lg);
+            sym_ptr = sym_src;
+        } else {
+            p.legacy_sym = w.legacy_sym ? 1 : 0;
+        }
+    } else {
+        p.T = 16; p.Gv = 32;
+    }
+    p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+    p.hot_first = a->hot_first ? 1 : 0;
+    p.N = pl.N;
+    p.n_wsplit = pl.n_wsplit; p.n_hsplit = pl.n_hsplit; p.nsplit = pl.nsplit;
+    p.wsplit_len = pl.wsplit_len; p.hsplit_len = pl.hsplit_len;
+    p.out = (_Float16 *)a->out;
+    p.attn_out = a->attn_weights;
+    p.stash = a->attn_weights ? a->attn_weights : (a->scores ? stash_ws : nullptr);
+    p.scores = a->scores;
+    p.n_scores = a->scores ? a->n_scores : 0;
+    p.decay = a->decay;
+    hipError_t e = akv::decode_launch(p, kb, vb, wk, sym_ptr, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "decode launch");
+    return ok();
+}
+
+int akv_quant_pack(const akv_quant_args *a, void *stream) {
+    if (!a) return fail(AKV_E_INVALID, "args is NULL");
+    if (a->abi_version != AKV_ABI_VERSION) return fail(AKV_E_ABI, "ABI mismatch");
+    if (a->D != 64 && a->D != 128) return fail(AKV_E_SHAPE, "head_dim %d unsupported (64 or 128)", a->D);
+    if (a->B < 1 || a->H < 1 || a->n_src < 0 || a->n_sel < 0) return fail(AKV_E_SHAPE, "bad sizes");
+    if (a->in_dtype < 0 || a->in_dtype > 2) return fail(AKV_E_DTYPE, "bad input dtype");
+    if (a->n_sel == 0) return ok();
+    if (!a->sel && a->n_sel > a->n_src) return fail(AKV_E_SHAPE, "n_sel > n_src without indices");
+    const bool affine = a->layout == AKV_QUANT_AFFINE;
+    const bool kvq = a->layout == AKV_QUANT_KVQ;
+    if (!affine && !kvq && a->layout != AKV_QUANT_TOKEN_GROUPS) return fail(AKV_E_INVALID, "unknown layout");
+    for (int bits : {a->bits_k, a->bits_v}) {
+        const bool okb = affine ? (bits >= 2 && bits <= 4)
+                                : kvq ? (bits == 2 || bits == 4 || bits == 8) : (bits >= 2 && bits <= 4) || bits == 8;
+        if (!okb) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
+    }
+    if (a->group_v != 32 && a->group_v != 64 && a->group_v != 128) return fail(AKV_E_UNSUPPORTED, "group_v must be 32, 64 or 128");
+    if (affine && a->D % a->group_v) return fail(AKV_E_SHAPE, "group_v must divide D");
+    if (a->block_t < 1) return fail(AKV_E_SHAPE, "block_t must be >= 1");
+    if (a->n_out < 0 || a->n_out > a->D || (a->n_out > 0 && !affine)) return fail(AKV_E_SHAPE, "bad n_out");
+    if (a->k && (!a->k_codes || !a->k_scale || !a->k_zero)) return fail(AKV_E_INVALID, "K outputs missing");
+    if (a->v && (!a->v_codes || !a->v_scale || !a->v_zero)) return fail(AKV_E_INVALID, "V outputs missing");
+    if (a->n_out > 0 && ((a->k && (!a->k_oidx || !a->k_odata)) || (a->v && (!a->v_oidx || !a->v_odata))))
+        return fail(AKV_E_INVALID, "outlier outputs missing");
+    for (const void *ptr : {(const void *)a->k_codes, (const void *)a->v_codes})
+        if (ptr && !aligned16(ptr)) return fail(AKV_E_ALIGN, "code outputs must be 16-byte aligned");
+    akv::QuantParams p{};
+    p.B = a->B; p.H = a->H; p.D = a->D;
+    p.in_dt = a->in_dtype;
+    // arithmetic dtype and the scale clamp as that dtype rounds it
+    p.ar_dt = kvq ? AKV_DT_F32 : a->in_dtype;
+    if (kvq) p.lo = 1e-10f;
+    else if (p.ar_dt == AKV_DT_F16) p.lo = 0.0f;  // 1e-8 underflows in fp16
+    else if (p.ar_dt == AKV_DT_BF16) p.lo = __builtin_bit_cast(float, 0x322c0000u);  // bfloat16(1e-8)
+    else p.lo = 1e-8f;
+    p.symmetric = kvq && a->symmetric;
+    p.k = a->k; p.v = a->v;
+    p.n_src = a->n_src; p.n_sel = a->n_sel; p.sel = a->sel;
+    p.bits_k = a->bits_k; p.bits_v = a->bits_v;
+    p.G_v = a->group_v;
+    p.n_out = a->n_out;
+    p.k_codes = a->k_codes; p.k_scale = a->k_scale; p.k_zero = a->k_zero;
+    p.v_codes = a->v_codes; p.v_scale = a->v_scale; p.v_zero = a->v_zero;
+    p.k_oidx = a->k_oidx; p.v_oidx = a->v_oidx; p.k_odata = a->k_odata; p.v_odata = a->v_odata;
+    if (affine) {
+        p.pD = a->D;
+        p.k_mode = 0;
+        p.T = a->block_t;
+        p.G_k = a->group_v;
+        p.sbits_k = a->bits_k; p.sbits_v = a->bits_v;
+        p.meta_dt = AKV_DT_F16;
+    } else {
+        p.pD = (int)round_up(a->D, a->group_v);
+        p.k_mode = 1;
+        p.T = 32;
+        p.G_k = a->group_v;
+        p.sbits_k = (a->bits_k == 2 || a->bits_k == 4) ? a->bits_k : 8;
+        p.sbits_v = (a->bits_v == 2 || a->bits_v == 4) ? a->bits_v : 8;
+        p.meta_dt = a->in_dtype;
+    }
+    p.k_row = p.pD * p.sbits_k / 8;
+    p.v_row = p.pD * p.sbits_v / 8;
+    p.nblk = (a->n_sel + p.T - 1) / p.T;
+    hipError_t e = akv::quant_launch(p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "quant launch");
+    return ok();
+}
+
+int akv_dequant_unpack(const akv_dequant_args *a, void *stream) {
+    if (!a) return fail(AKV_E_INVALID, "args is NULL");
+    if (a->abi_version != AKV_ABI_VERSION) return fail(AKV_E_ABI, "ABI mismatch");
+    const akv_warm_desc &w = a->warm;
+    if (a->D % 8 || a->D < 8) return fail(AKV_E_SHAPE, "D must be a positive multiple of 8");
+    if (w.n_warm < 0) return fail(AKV_E_SHAPE, "n_warm < 0");
+    akv::DequantParams p{};
+    p.kind = w.kind;
+    p.D = a->D;
+    p.n_warm = w.n_warm;
+    p.bits_k = w.bits_k; p.bits_v = w.bits_v;
+    p.kc = w.k_codes; p.vc = w.v_codes;
+    p.ks = w.k_scale; p.kz = w.k_zero; p.vs = w.v_scale; p.vz = w.v_zero;
+    p.out_dt = a->out_dtype;
+    p.k_out = a->k_out; p.v_out = a->v_out;
+    if (w.kind == AKV_WARM_AFFINE) {
+        for (int bits : {w.bits_k, w.bits_v})
+            if (bits < 2 || bits > 4) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
+        if (w.block_t < 1 || w.group_v < 1 || a->D % w.group_v) return fail(AKV_E_SHAPE, "bad block_t / group_v");
+        if (a->out_dtype != AKV_DT_F16) return fail(AKV_E_DTYPE, "affine dequant produces float16");
+        p.nbh = a->B * a->Hkv; p.Hkv = a->Hkv;
+        p.kc_row = a->D * w.bits_k / 8; p.vc_row = a->D * w.bits_v / 8;
+        p.T = w.block_t; p.Gv = w.group_v;
+        p.nblk = (w.n_warm + w.block_t - 1) / w.block_t;
+        p.n_out = w.n_out;
+        p.k_oidx = w.k_oidx; p.v_oidx = w.v_oidx; p.k_odata = w.k_odata; p.v_odata = w.v_odata;
+    } else if (w.kind == AKV_WARM_LEGACY) {
+        if (w.bits_k != w.bits_v) return fail(AKV_E_BITS, "legacy warm tier uses one width for K and V");
+        if (w.bits_k != 2 && w.bits_k != 4 && w.bits_k != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", w.bits_k);
+        if (w.group_size < 1) return fail(AKV_E_SHAPE, "bad group_size");
+        if (a->out_dtype < 0 || a->out_dtype > 2) return fail(AKV_E_DTYPE, "bad out dtype");
+        const int pD = (int)round_up(a->D, w.group_size);
+        p.nbh = w.warm_heads; p.Hkv = w.warm_heads;
+        p.kc_row = p.vc_row = pD * w.bits_k / 8;
+        p.gs = w.group_size; p.lg = pD / w.group_size; p.meta_dt = w.meta_dtype;
+        p.legacy_sym = w.legacy_sym;
+        if (w.legacy_sym < 0) {
+            if (!a->workspace || !aligned16(a->workspace))
+                return fail(AKV_E_WORKSPACE, "symmetric-branch detection needs a 256-byte workspace");
+            p.sym_flags = (const int *)a->workspace;
+            hipError_t e = akv::legacy_sym_launch(w.k_zero, w.v_zero, (int64_t)w.warm_heads * w.n_warm * p.lg,
+                                                  w.meta_dtype, (int *)a->workspace, (hipStream_t)stream);
+            if (e != hipSuccess) return hip_fail(e, "legacy symmetric detection");
+        }
+    } else {
+        return fail(AKV_E_INVALID, "unknown warm kind %d", w.kind);
+    }
+    hipError_t e = akv::dequant_launch(p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dequant launch");
+    return ok();
+}
+
+int akv_bitpack(const void *codes, void *packed, int64_t rows, int32_t dim, int32_t bits, void *stream) {
+    if (bits != 2 && bits != 3 && bits != 4) return fail(AKV_E_BITS, "bitpack handles 2/3/4 bits, got %d", bits);
+    if (rows < 0 || dim < 0) return fail(AKV_E_SHAPE, "bad sizes");
+    if ((rows > 0 && dim > 0) && (!codes || !packed)) return fail(AKV_E_INVALID, "null pointer");
+    const int prow = bits == 4 ? (dim + 1) / 2 : bits == 2 ? (dim + 3) / 4 : 3 * ((dim + 7) / 8);
+    hipError_t e = akv::bitpack_launch(codes, packed, rows, dim, bits, prow, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "bitpack launch");
+    return ok();
+}
+
+int akv_bitunpack(const void *packed, void *codes, int64_t rows, int32_t packed_dim, int32_t orig_dim, int32_t bits,
+                  void *stream) {
+    if (bits != 2 && bits != 3 && bits != 4) return fail(AKV_E_BITS, "bitunpack handles 2/3/4 bits, got %d", bits);
+    if (rows < 0 || packed_dim < 0 || orig_dim < 0) return fail(AKV_E_SHAPE, "bad sizes");
+    const int cap = bits == 4 ? 2 * packed_dim : bits == 2 ? 4 * packed_dim : 8 * (packed_dim / 3);
+    if (bits == 2 && orig_dim != 4 * packed_dim) return fail(AKV_E_SHAPE, "2-bit unpack needs orig_dim == 4 * packed_dim");
+    if (orig_dim > cap) return fail(AKV_E_SHAPE, "orig_dim %d exceeds the %d packed codes", orig_dim, cap);
+    if ((rows > 0 && orig_dim > 0) && (!codes || !packed)) return fail(AKV_E_INVALID, "null pointer");
+    hipError_t e = akv::bitunpack_launch(packed, codes, rows, packed_dim, orig_dim, bits, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "bitunpack launch");
+    return ok();
+}
+
+int akv_importance_update(const akv_importance_args *a, void *stream) {
+    if (!a) return fail(AKV_E_INVALID, "args is NULL");
+    if (a->abi_version != AKV_ABI_VERSION) return fail(AKV_E_ABI, "ABI mismatch");
+    if (a->attn_dtype < 0 || a->attn_dtype > 2) return fail(AKV_E_DTYPE, "bad attention dtype");
+    if (a->B < 1 || a->H < 1 || a->M < 1 || a->N < 0 || a->n_scores < 0) return fail(AKV_E_SHAPE, "bad sizes");
+    if ((a->n_scores > 0 && !a->scores) || (a->N > 0 && !a->attn)) return fail(AKV_E_INVALID, "null pointer");
+    akv::ImportanceParams p{};
+    p.attn = a->attn; p.attn_dt = a->attn_dtype;
+    p.B = a->B; p.H = a->H; p.M = a->M; p.N = a->N;
+    p.scores = a->scores; p.n_scores = a->n_scores; p.decay = a->decay;
+    hipError_t e = akv::importance_launch(p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "importance launch");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,56 @@
+// Host/device parameter block of the split-K decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace akv {
+
+struct DecodeParams {
+    // shapes
+    int B, Hq, Hkv, M, D, g, R, nchunk, prows;  // prows = min(16, R): rows per partial
+    // query / hot tier (fp16)
+    const _Float16 *q;
+    const _Float16 *khot, *vhot;
+    int64_t n_hot;
+    // warm tier
+    const void *kc, *vc;          // packed codes
+    const void *ks, *kz, *vs, *vz; // meta
+    int64_t n_warm;
+    int kc_row, vc_row;           // bytes per packed row
+    int T, Gv;                    // affine: K token block, V channel group
+    int64_t nblk;                 // affine: K blocks per (b, kv-head)
+    int n_out;                    // affine outliers per block
+    const int64_t *k_oidx, *v_oidx;
+    const _Float16 *k_odata, *v_odata;
+    int gs, lg, meta_dt;          // legacy: group size, groups per row, meta dtype
+    int warm_heads;               // legacy: 1 or Hkv
+    int legacy_sym;               // legacy: 0/1 when forced
+    const int *sym_flags;         // legacy: device flags [K, V] when detected
+    float half_max_k, half_max_v; // legacy: maxv // 2
+    // softmax
+    float scale_log2;             // sm_scale * log2(e)
+    int hot_first;
+    int64_t N;                    // logical tokens n_hot + n_warm
+    // split schedule
+    int n_wsplit, n_hsplit, nsplit;
+    int64_t wsplit_len, hsplit_len;
+    // outputs / workspace
+    float *part;                  // split partials
+    float *stash;                 // [B][Hq][M][N] log2-domain logits (or null)
+    float *rowstats;              // [B*Hq*M][2] (M, L)
+    _Float16 *out;                // [B][Hq][M][D]
+    float *attn_out;              // normalised weights (or null)
+    float *scores;                // importance EMA (or null)
+    int64_t n_scores;
+    float decay;
+};
+
+// Launch split + reduce (+ weights/importance) kernels.  `sym_src` = {meta dtype, count}
+// of the legacy zero-point tensors when the symmetric branch must be detected.
+// flags[0] (K) / flags[1] (V) = 1 iff every zero-point is 0 (the reference's symmetric branch).
+hipError_t legacy_sym_launch(const void *kz, const void *vz, int64_t n, int dt, int *flags, hipStream_t s);
+
+hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const int *sym_src, hipStream_t s);
+
+}  // namespace akv

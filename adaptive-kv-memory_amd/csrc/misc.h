@@ -1,0 +1,42 @@
+// Parameter blocks of the dequant, bitpack and importance kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace akv {
+
+struct DequantParams {
+    int kind;                     // AKV_WARM_AFFINE / AKV_WARM_LEGACY
+    int nbh, Hkv, D;              // rows are (bh, token); nbh = B*Hkv (affine) or Hw (legacy)
+    int64_t n_warm;
+    int bits_k, bits_v;
+    const void *kc, *vc;
+    int kc_row, vc_row;
+    const void *ks, *kz, *vs, *vz;
+    int T, Gv;                    // affine
+    int64_t nblk;
+    int n_out;
+    const int64_t *k_oidx, *v_oidx;
+    const void *k_odata, *v_odata;
+    int gs, lg, meta_dt, legacy_sym;  // legacy
+    const int *sym_flags;
+    int out_dt;
+    void *k_out, *v_out;
+};
+
+struct ImportanceParams {
+    const void *attn;
+    int attn_dt;
+    int64_t B, H, M, N;
+    float *scores;
+    int64_t n_scores;
+    float decay;
+};
+
+hipError_t dequant_launch(const DequantParams &p, hipStream_t s);
+hipError_t bitpack_launch(const void *codes, void *packed, int64_t rows, int dim, int bits, int prow, hipStream_t s);
+hipError_t bitunpack_launch(const void *packed, void *codes, int64_t rows, int prow, int dim, int bits, hipStream_t s);
+hipError_t importance_launch(const ImportanceParams &p, hipStream_t s);
+
+}  // namespace akv

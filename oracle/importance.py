@@ -1,0 +1,69 @@
+"""Oracle restatement of the attention-sum importance update.
+
+``fused_importance_update`` (akv/triton_ops.py:604-650, the torch path):
+    imp = attn.float().mean(dim=(0, 1)).sum(dim=0)       # (N,)
+    truncate imp to len(scores) or zero-pad it
+    scores.mul_(decay).add_(imp)                         # in place, returned
+(The Triton kernel at akv/triton_ops.py:288-323 divides by M; the torch path
+and ``ImportanceScorer`` sum over queries -- the sum is followed here.)
+
+``ImportanceScorer.update`` accumulate strategies (akv/importance.py:73-164):
+ATTENTION_ACCUMULATION and IMPORTANCE apply the same EMA on the first kv_len
+scores (growing the per-layer score vector with zeros); OBSERVATION_WINDOW
+sums only the last ``observation_window`` queries and average-pools with
+``pooling_kernel`` (count_include_pad) before the EMA.
+
+Pinning: the decay KAT ``ones(32)``, zero attention, decay 0.5 -> 0.5
+(tests/test_triton_ops.py:169-174); float64 evaluation of the closed form;
+sum-over-queries vs mean checked at M > 1.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+
+def importance_from_attn(attn: np.ndarray) -> np.ndarray:
+    a = np.asarray(attn, dtype=np.float32)
+    return a.mean(axis=(0, 1), dtype=np.float32).sum(axis=0, dtype=np.float32)
+
+
+def fused_importance_update(attn: np.ndarray, scores: np.ndarray, decay: float = 0.95) -> np.ndarray:
+    """akv/triton_ops.py:604-650 (returns the updated copy)."""
+    imp = importance_from_attn(attn)
+    n = scores.shape[0]
+    if imp.shape[0] > n:
+        imp = imp[:n]
+    elif imp.shape[0] < n:
+        imp = np.concatenate([imp, np.zeros(n - imp.shape[0], np.float32)])
+    s = np.asarray(scores, dtype=np.float32) * np.float32(decay)
+    return (s.astype(np.float32) + imp).astype(np.float32)
+
+
+def scorer_update(scores, attn, strategy="attention_accumulation", decay=0.95,
+                  observation_window=32, pooling_kernel=7):
+    """akv/importance.py:73-164 for the accumulate strategies; returns new scores."""
+    a = np.asarray(attn, dtype=np.float32)
+    avg = a.mean(axis=(0, 1), dtype=np.float32)  # (M, N)
+    key_imp = avg.sum(axis=0, dtype=np.float32)
+    kv_len = key_imp.shape[0]
+    if strategy == "observation_window":
+        ql = avg.shape[0]
+        w = min(observation_window, ql)
+        key_imp = avg[ql - w:, :].sum(axis=0, dtype=np.float32)
+        ks = pooling_kernel
+        if ks > 1 and kv_len > ks:
+            pad = ks // 2
+            xp = np.concatenate([np.zeros(pad, np.float32), key_imp, np.zeros(pad, np.float32)])
+            L = xp.shape[0] - ks + 1
+            pooled = np.array([xp[i:i + ks].sum(dtype=np.float32) for i in range(L)], np.float32) / np.float32(ks)
+            key_imp = pooled[:kv_len].astype(np.float32)
+    elif strategy not in ("attention_accumulation", "importance"):
+        raise ValueError(f"strategy {strategy} is not an accumulate strategy")
+    if scores is None or scores.shape[0] < kv_len:
+        new = np.zeros(kv_len, np.float32)
+        if scores is not None:
+            new[: scores.shape[0]] = scores
+        scores = new
+    scores = np.array(scores, dtype=np.float32, copy=True)
+    scores[:kv_len] = (scores[:kv_len] * np.float32(decay)).astype(np.float32) + key_imp
+    return scores

@@ -1,0 +1,145 @@
+"""Fused dequant-attention on the device vs the oracle's fp32 dequant-attention.
+
+Tolerance (from the task statement): 2e-3 max-abs, 1e-3 mean-abs against the
+fp32 attention over the oracle's fp16 dequantized K/V."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce, assert_close_attn, to_dev, warm_from_oracle
+from oracle import affine as oaff
+from oracle import attention as oatt
+from oracle import importance as oimp
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(B, Hq, Hkv, D, Nh, Nw, bk, bv, T=32, G=32, of=0.0, M=1, seed=0, outl=2, heavy=0):
+    from akv import workloads as wl
+    shape = wl.DecodeShape("t", B, Hq, Hkv, D, Nh, Nw, bk, bv, outlier_fraction=of, k_outlier_channels=outl,
+                           heavy_tail_channels=heavy, block_t=T, group_v=G, M=M)
+    k, v = wl.make_kv(shape, layer=seed)
+    q = wl.make_q(shape, layer=seed)
+    (kw, vw), (kh, vh) = wl.split_hot_warm(k, v, Nh)
+    w = oaff.quantize_kv_blocked(kw.numpy(), vw.numpy(), bk, bv, T, G, of)
+    kd, vd = oaff.dequant_kv_blocked(w)
+    return q.numpy(), kh.numpy(), vh.numpy(), w, kd, vd
+
+
+def _run(q, kh, vh, w, hot_first, **kw):
+    import akv
+    wt = warm_from_oracle(w) if w is not None else None
+    return akv.decode_attention(to_dev(q), to_dev(kh) if kh is not None else None,
+                                to_dev(vh) if vh is not None else None, wt, hot_first=hot_first, **kw)
+
+
+@pytest.mark.parametrize("bk,bv", [(4, 4), (3, 3), (2, 2), (4, 2), (4, 3), (3, 2)])
+def test_qwen_4k_shape(bk, bv):
+    announce(f"decode Qwen 4k shape bits={bk}/{bv}")
+    q, kh, vh, w, kd, vd = _case(1, 12, 2, 128, 512, 3584, bk, bv)
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+@pytest.mark.parametrize("hot_first", [False, True])
+def test_weights_and_importance(hot_first):
+    announce(f"decode weights+importance hot_first={hot_first}")
+    q, kh, vh, w, kd, vd = _case(2, 12, 2, 128, 100, 700, 3, 3, seed=1)
+    N = 800
+    scores0 = np.random.default_rng(0).random(N + 37).astype(np.float32)
+    sc = to_dev(scores0)
+    out, attn = _run(q, kh, vh, w, hot_first, scores=sc, decay=0.9, return_weights=True)
+    ref, ref_attn = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=hot_first)
+    assert_close_attn(out, ref)
+    a = attn.cpu().numpy()
+    np.testing.assert_allclose(a, ref_attn, atol=2e-6, rtol=1e-4)
+    np.testing.assert_allclose(a.sum(-1), 1.0, atol=1e-5)
+    ref_sc = oimp.fused_importance_update(ref_attn, scores0, 0.9)
+    np.testing.assert_allclose(sc.cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-6)
+
+
+def test_importance_without_weights_matches():
+    announce("decode importance (stash in workspace)")
+    q, kh, vh, w, kd, vd = _case(2, 12, 2, 128, 64, 448, 4, 4, seed=2)
+    s0 = np.zeros(512, np.float32)
+    sc = to_dev(s0)
+    _run(q, kh, vh, w, False, scores=sc, decay=0.9)
+    _, ref_attn = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False)
+    np.testing.assert_allclose(sc.cpu().numpy(), oimp.fused_importance_update(ref_attn, s0, 0.9),
+                               rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("Hq,Hkv,M", [(32, 32, 1), (8, 2, 1), (4, 1, 1), (12, 2, 3), (2, 2, 9)])
+def test_head_groupings(Hq, Hkv, M):
+    announce(f"decode Hq={Hq} Hkv={Hkv} M={M}")
+    q, kh, vh, w, kd, vd = _case(2, Hq, Hkv, 128, 48, 320, 4, 2, M=M, seed=3)
+    out = _run(q, kh, vh, w, hot_first=True)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=True, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+def test_outlier_channels_heavy_tails():
+    announce("decode outliers + heavy tails (Llama-7B shape, small)")
+    q, kh, vh, w, kd, vd = _case(2, 32, 32, 128, 64, 512, 4, 2, of=0.01, outl=0, heavy=4, seed=4)
+    assert w["n_out"] == 1
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+@pytest.mark.parametrize("D", [64])
+def test_head_dim_64(D):
+    announce("decode D=64")
+    q, kh, vh, w, kd, vd = _case(1, 4, 2, D, 32, 224, 3, 4, seed=5)
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+def test_ragged_tails_and_tiny_hot():
+    announce("decode ragged warm tail, 5 hot tokens")
+    q, kh, vh, w, kd, vd = _case(1, 6, 3, 128, 5, 75, 3, 3, seed=6)  # 75 warm: partial block
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+def test_hot_only_and_warm_only():
+    announce("decode hot only / warm only")
+    q, kh, vh, w, kd, vd = _case(1, 4, 2, 128, 40, 96, 4, 4, seed=7)
+    out = _run(q, kh, vh, None, hot_first=True)
+    ref, _ = oatt.attention_fp32(q, kh, vh, return_weights=False)
+    assert_close_attn(out, ref)
+    out = _run(q, None, None, w, hot_first=True)
+    ref, _ = oatt.attention_fp32(q, kd, vd, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+def test_split_counts_agree():
+    announce("decode split counts")
+    q, kh, vh, w, kd, vd = _case(1, 12, 2, 128, 256, 2048, 3, 3, seed=8)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    for ns in (1, 3, 16, 200):
+        assert_close_attn(_run(q, kh, vh, w, False, num_splits=ns), ref)
+
+
+def test_full_size_qwen_32k_slice():
+    """One layer of the 32k workload at full size; the oracle checks one batch element."""
+    import akv
+    from akv import workloads as wl
+    announce("decode Qwen 32k full-size layer")
+    shape = wl.QWEN_DECODE_32K
+    k, v = wl.make_kv(shape, device="cuda")
+    q = wl.make_q(shape, device="cuda")
+    (kw, vw), (kh, vh) = wl.split_hot_warm(k, v, shape.n_hot)
+    wt = akv.quantize_kv(kw, vw, shape.bits_k, shape.bits_v, shape.block_t, shape.group_v)
+    out = akv.decode_attention(q, kh, vh, wt, hot_first=False)
+    b = 5
+    w1 = oaff.quantize_kv_blocked(kw[b:b + 1].cpu().numpy(), vw[b:b + 1].cpu().numpy(), 3, 3, 32, 32)
+    # the device tier of batch b is the oracle's, byte for byte
+    assert np.array_equal(wt.k_codes[b:b + 1].cpu().numpy(), w1["k_codes"])
+    kd, vd = oaff.dequant_kv_blocked(w1)
+    ref, _ = oatt.mixed_attention_fp32(q[b:b + 1].cpu().numpy(), kh[b:b + 1].cpu().numpy(),
+                                       vh[b:b + 1].cpu().numpy(), kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out[b:b + 1], ref)

@@ -1,0 +1,68 @@
+"""Host-side behaviour of the akv package that needs no GPU: presets, errors,
+refusal of CPU tensors (there is no CPU path)."""
+import pytest
+import torch
+
+
+def test_presets_table():
+    import akv
+    p = akv._PRESETS
+    assert set(p) == {"quality", "balanced", "compact", "k4v2", "k4v3"}
+    assert (p["quality"]["warm_bits"], p["quality"]["hot_budget"]) == (4, 256)
+    assert (p["balanced"]["warm_bits"], p["balanced"]["hot_budget"]) == (3, 128)
+    assert (p["compact"]["warm_bits"], p["compact"]["hot_budget"]) == (2, 64)
+    assert (p["k4v2"]["warm_key_bits"], p["k4v2"]["warm_value_bits"]) == (4, 2)
+    assert (p["k4v3"]["warm_key_bits"], p["k4v3"]["warm_value_bits"]) == (4, 3)
+
+
+def test_preset_resolution_and_errors():
+    import akv
+    c = akv.AKVCache(preset="k4v2")
+    assert (c.warm_bits, c.hot_budget, c.warm_key_bits, c.warm_value_bits) == (4, 128, 4, 2)
+    c = akv.AKVCache(preset="balanced")
+    assert (c.warm_key_bits, c.warm_value_bits, c.group_size, c.outlier_fraction) == (3, 3, 64, 0.0)
+    c = akv.AKVCache(warm_bits=2, hot_budget=32, warm_value_bits=4)
+    assert (c.warm_key_bits, c.warm_value_bits) == (2, 4)
+    c = akv.AKVCache()
+    assert (c.warm_bits, c.hot_budget) == (3, 128)
+    with pytest.raises(ValueError, match="Unknown preset"):
+        akv.AKVCache(preset="nope")
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        akv.AKVCache(preset="quality", warm_bits=4)
+    with pytest.raises(ValueError, match="mutually exclusive"):
+        akv.AKVCache(preset="quality", hot_budget=8)
+
+
+def test_cpu_tensors_are_refused():
+    import akv
+    k = torch.zeros(1, 1, 32, 128, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        akv.quantize_kv(k, k)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        akv.pack(torch.zeros(2, 8, dtype=torch.uint8), 4)
+    q = torch.zeros(1, 2, 1, 64, dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        akv.fused_decode_attention(torch.zeros(1, 2, 2, 64, dtype=torch.float16), q, q)
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        akv.fused_decode_attention(q, torch.zeros(1, 2, 4, 64, dtype=torch.float16),
+                                   torch.zeros(1, 2, 4, 64, dtype=torch.float16))
+
+
+def test_legacy_bits_and_config_errors():
+    import akv
+    with pytest.raises(ValueError):
+        akv.QuantConfig(bits=3)
+    with pytest.raises(ValueError):
+        akv.QuantConfig(group_size=0)
+    assert akv.HAS_TRITON is False
+
+
+def test_workload_shapes():
+    from akv import workloads as wl
+    s = wl.QWEN_DECODE_32K
+    assert (s.B, s.Hq, s.Hkv, s.N, s.n_hot, s.bits_k, s.layers, s.decay) == (8, 12, 2, 32768, 1024, 3, 28, 0.9)
+    k, v = wl.make_kv(wl.DecodeShape("t", 1, 2, 2, 128, 4, 60, 3, 3, k_outlier_channels=2))
+    assert k.dtype == torch.float16 and k.shape == (1, 2, 64, 128)
+    # two channels per head scaled x10
+    std = k.float().std(dim=2)[0]
+    assert int((std > 5).sum()) == 4
