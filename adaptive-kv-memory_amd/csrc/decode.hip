@@ -1,51 +1,37 @@
 // Split-K fused dequant-attention over a hot fp16 + warm packed KV cache.
 //
-// Grid: (split, kv-head, batch * row-chunk).  A workgroup owns one
+// Grid: (split, kv-head, batch * row-chunk).  A workgroup (4 waves) owns one
 // (batch, kv-head) and one contiguous token range of either the warm or the
 // hot segment.  Its query rows are the Hq/Hkv query heads (x M query
 // positions) that share the kv head -- up to 16 rows, the N dimension of the
 // matrix-core tiles, so every K/V byte loaded feeds all of them.
 //
-// Per 16-token tile a wave:
-//   QK:  S^T[16 tok x 16 rows] = K_tile . Q^T  -- 16x16x32 f16 MFMA; each lane
-//        dequantizes the codes of one token for D/4 channels straight from
-//        the packed row into the A operand (no LDS), K scale/zero pairs come
-//        from a per-block LDS copy laid out in pair order.
-//   softmax: online, log2 domain, lazy rescale (only when a row max grows by
-//        more than 8); probabilities go to fp16 scaled by 2^7.
-//   PV:  O^T[16 chunks x 16 rows] += V^T . P^T -- 16x16x16 f16 MFMA; the A
-//        operand holds 4 tokens x 1 channel, so each lane reads one 8-channel
-//        chunk of 4 tokens and builds (token, token) half pairs.
-// Waves merge in LDS; one (m, l, acc) partial per workgroup goes to the
-// workspace and akv_reduce_kernel merges the splits (log-sum-exp).
+// Per 16-token tile a wave does:
+//   QK:  S^T[16 tok x 16 rows] = K_tile . Q^T with 16x16x32 f16 MFMA.  Lane
+//        (token l%16, group l/16) dequantizes D/4 channels of its token
+//        straight from the packed row into the A operand.  Codes are moved
+//        into fp16 halves with byte permutes and one and-or against the
+//        0x6400 exponent; a code sitting 2^o above bit 0 is multiplied by a
+//        block scale pre-divided by 2^o (exact whenever that scale is
+//        representable, checked per block; otherwise codes are shifted down).
+//        The Q operand is permuted to the channel order the codes come out in.
+//   softmax: online in the log2 domain with a lazy rescale (only when a row
+//        max grows by more than 8); probabilities enter the PV product as
+//        fp16 scaled by 2^7.
+//   PV:  O^T[16 chunks x 16 rows] += V^T . P^T with 16x16x16 f16 MFMA.  Lane
+//        (chunk l%16, tokens 4*(l/16)..+3) reads one 8-channel chunk of 4
+//        tokens and forms (token, token) half pairs.
+// Loads of tile i+1 (codes and scale/zero) are issued before tile i is
+// computed.  Waves merge in LDS; one (m, l, acc) partial per workgroup goes to
+// the workspace and decode_reduce_kernel merges the splits (log-sum-exp).
 #include "akv_common.h"
 #include "decode.h"
 
 namespace akv {
 
-constexpr int kThresh = 8;     // lazy-rescale threshold (log2 units)
-constexpr float kPScale = 128.0f;  // fp16 probabilities carry a 2^7 factor
-
-template <int D>
-struct Geo {
-    static constexpr int KSTEPS = D / 32;       // QK MFMA k-steps
-    static constexpr int LCH = D / 4;           // K channels per lane group
-    static constexpr int NPAIRS = LCH / 2;      // K code pairs per lane
-    static constexpr int VCH = D / 8;           // 8-channel V chunks (MFMA rows used)
-};
-
-template <int BITS>
-struct KRaw {  // raw K code dwords a lane holds for one token
-    static constexpr int bytes(int lch) { return lch * BITS / 8; }
-};
-
-// LDS layout of one wave's staging area (bytes)
-template <int D>
-struct WaveLds {
-    static constexpr int KMETA = 2 * 4 * (D / 8) * 4;  // [s|z][grp][pair] u32
-    static constexpr int VMETA = 2 * 16 * 16 * 4;      // [s|z][group<=16][16 tokens] f32 or f16
-    static constexpr int BYTES = KMETA + VMETA;
-};
+constexpr float kThresh = 8.0f;    // lazy-rescale threshold (log2 units)
+constexpr float kPLog2 = 7.0f;     // fp16 probabilities carry a 2^7 factor
+constexpr int kNW = 4;             // waves per workgroup
 
 __device__ __forceinline__ float wave_max16(float x) {
     x = fmaxf(x, __shfl_xor(x, 16));
@@ -58,56 +44,229 @@ __device__ __forceinline__ float wave_sum16(float x) {
     return x;
 }
 
-template <int D>
-struct WaveState {
-    float m;        // running max (log2 domain) of this lane's row
-    float l;        // partial sum of exp2(s - m) over this lane's tokens
-    f4 acc[8];      // O^T: acc[j][i] = chunk (4*grp+i), channel slot j, row col
+// (x & m) | c in one VALU op (GFX9 VOP3 takes no literals, so the compiler
+// otherwise splits it into and + or).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "s"(c));
+    return r;
+}
+
+constexpr uint32_t kMagic = 0x64006400u;
+
+// ---------------------------------------------------------------------------
+// K side (lane = one token, LCH = D/4 channels).  Pair pi of the lane's codes
+// lives in a window dword at bit offset koff (both halves); its channels are
+// kpair_chan<KB>(pi, 0/1).
+// ---------------------------------------------------------------------------
+template <int KB>
+__host__ __device__ constexpr int koff(int pi) {
+    if (KB == 3) {
+        return (pi % 8) == 0 ? 0 : (pi % 8) == 1 ? 3 : (pi % 8) == 2 ? 6 : (pi % 8) == 3 ? 1
+             : (pi % 8) == 4 ? 4 : (pi % 8) == 5 ? 7 : (pi % 8) == 6 ? 2 : 5;
+    } else if (KB == 4) {
+        return (pi % 2) * 4;
+    } else if (KB == 2) {
+        return 2 * (pi % 4);
+    }
+    return 0;
+}
+
+// windows: 3-bit -> 3 per word pair, 4-bit / 2-bit -> 2 per dword
+template <int KB>
+struct KWin {
+    uint32_t w[(KB == 3) ? 6 : (KB == 4 ? 8 : 4)];
 };
 
-// One tile's softmax + PV given S^T (this lane: tokens 4*grp+i, row col) and
-// the V^T operands vop[j] (chunk col, tokens 4*grp..+3, channel slot j).
-template <int D>
-__device__ __forceinline__ void softmax_pv(WaveState<D> &st, f4 s, const h4 *vop) {
-    float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    tmax = wave_max16(tmax);
-    const bool need = tmax > st.m + (float)kThresh;
-    if (__builtin_amdgcn_ballot_w64(need)) {  // wave-uniform
-        const float mn = fmaxf(st.m, tmax);
-        const float alpha = (mn == -INFINITY) ? 1.0f : exp2f(st.m - mn);
+template <int KB, int NP>
+__device__ __forceinline__ void k_windows(const uint32_t *r, KWin<KB> &W) {
+    if (KB == 3) {
+        // word pair 0: bytes b0..b5 (r0 = b0..b3, r1 = b4..b7); pair 1: b6..b11
+        W.w[0] = perm(r[1], r[0], 0x04050102u);  // [b2 b1 | b5 b4]  W[15:0]
+        W.w[1] = perm(r[1], r[0], 0x03040001u);  // [b1 b0 | b4 b3]  W[23:8]
+        W.w[2] = perm(r[1], r[0], 0x0C030C00u);  // [b0 0  | b3 0 ]  W[23:16]
+        if (NP > 8) {
+            W.w[3] = perm(r[2], r[1], 0x06070304u);
+            W.w[4] = perm(r[2], r[1], 0x05060203u);
+            W.w[5] = perm(r[2], r[1], 0x0C050C02u);
+        }
+    } else if (KB == 4) {
+#pragma unroll
+        for (int d = 0; d < NP / 4; ++d) {
+            W.w[2 * d] = r[d];                               // bytes 0 | 2
+            W.w[2 * d + 1] = perm(0u, r[d], 0x0C030C01u);   // bytes 1 | 3
+        }
+    } else if (KB == 2) {
+#pragma unroll
+        for (int d = 0; d < NP / 8; ++d) {
+            W.w[2 * d] = r[d];
+            W.w[2 * d + 1] = perm(0u, r[d], 0x0C030C01u);
+        }
+    }
+}
+
+template <int KB>
+__device__ __forceinline__ uint32_t k_window_of(const KWin<KB> &W, int pi) {
+    if (KB == 3) {
+        const int k = pi % 8, base = 3 * (pi / 8);
+        return W.w[base + (k < 3 ? 0 : (k < 6 ? 1 : 2))];
+    } else if (KB == 4) {
+        return W.w[2 * (pi / 4) + ((pi % 4) >= 2 ? 1 : 0)];
+    } else {
+        return W.w[2 * (pi / 8) + ((pi % 8) >= 4 ? 1 : 0)];
+    }
+}
+
+template <int KB>
+__host__ __device__ constexpr uint32_t kmask(int pi) {
+    return (((KB == 3) ? 7u : (KB == 4 ? 15u : 3u)) << koff<KB>(pi)) * 0x00010001u;
+}
+
+// ---------------------------------------------------------------------------
+struct WaveState {
+    float m2;      // running max of this lane's row (log2 domain: q.k * sm_scale * log2 e)
+    float l;       // partial sum of 2^7 * exp2(s - m2) over this lane's tokens
+    f4 acc[8];     // O^T: acc[j][i] = chunk (4*grp+i), channel slot j, row col (x 2^7)
+};
+
+// online softmax over one tile.  s: raw q.k for tokens 4*grp+i of row col.
+// Returns the fp16 P^T operand (x 2^7); rescales the running state when needed.
+__device__ __forceinline__ h4 softmax_tile(WaveState &st, f4 s, float sl2) {
+    float t = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    t = wave_max16(t);
+    const float tm2 = t * sl2;
+    if (__builtin_amdgcn_ballot_w64(tm2 > st.m2 + kThresh)) {  // wave-uniform, rare after warm-up
+        const float mn = fmaxf(st.m2, tm2);
+        const float alpha = __builtin_amdgcn_exp2f(st.m2 - mn);
         st.l *= alpha;
 #pragma unroll
         for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
-        st.m = mn;
+        st.m2 = mn;
     }
+    const float bias = kPLog2 - st.m2;
     float p[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = (st.m == -INFINITY) ? 0.0f : exp2f(s[i] - st.m);
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, bias));
     st.l += (p[0] + p[1]) + (p[2] + p[3]);
-    h4 pop;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pop[i] = (_Float16)(p[i] * kPScale);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) st.acc[j] = mfma_k16(vop[j], pop, st.acc[j]);
+    return (h4){(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
 }
 
-template <int D>
-__device__ __forceinline__ void store_stash(const DecodeParams &p, int b, int row_valid, int h, int m,
-                                            int64_t nlog0, const f4 &s, const bool *valid) {
+__device__ __forceinline__ void store_stash(const DecodeParams &p, int64_t rowbase, int row_valid, int64_t nlog0,
+                                            f4 s, float sl2, int nvalid) {
     if (!p.stash || !row_valid) return;
-    float *dst = p.stash + ((int64_t)(b * p.Hq + h) * p.M + m) * p.N + nlog0;
+    float *dst = p.stash + rowbase + nlog0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (valid[i]) dst[i] = s[i];
+        if (i < nvalid) dst[i] = s[i] * sl2;
 }
 
+// raw loads of one warm tile
 template <int D, int KB, int VB, int WK>
-__global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p) {
-    using G = Geo<D>;
-    constexpr int NW = 4;
-    constexpr int KSTEPS = G::KSTEPS, LCH = G::LCH, NPAIRS = G::NPAIRS, VCH = G::VCH;
-    constexpr int KBYTES = LCH * KB / 8;       // warm K code bytes per lane
-    constexpr int KDW = (KBYTES + 3) / 4;
+struct WarmRaw {
+    static constexpr int KBYTES = (D / 4) * KB / 8;
+    static constexpr int KDW = (KBYTES + 3) / 4;
+    uint32_t k[KDW];
+    uint32_t v[4][VB == 8 ? 2 : 1];
+    uint32_t ms[4], mz[4];  // V meta staging values (fp16 bits or fp32 bits)
+    float lks[4], lkz[4];   // legacy K meta of this lane's token
+};
+
+template <int D, int KB, int VB, int WK>
+__device__ __forceinline__ void load_warm_tile(WarmRaw<D, KB, VB, WK> &R, const DecodeParams &p, int t0, int lane,
+                                               int col, int grp, __amdgpu_buffer_rsrc_t rkc,
+                                               __amdgpu_buffer_rsrc_t rvc, __amdgpu_buffer_rsrc_t rvs,
+                                               __amdgpu_buffer_rsrc_t rvz, int ngr, int nwarm, int64_t hw) {
+    constexpr int LCH = D / 4;
+    constexpr int KBYTES = WarmRaw<D, KB, VB, WK>::KBYTES;
+    constexpr int VCH = D / 8;
+    // K codes: lane's token t0+col, channels LCH*grp .. +LCH
+    {
+        const uint32_t off = (uint32_t)(t0 + col) * (uint32_t)p.kc_row + KBYTES * grp;
+        if (KBYTES == 12) { u3 x = bld96(rkc, off); R.k[0] = x[0]; R.k[1] = x[1]; R.k[2] = x[2]; }
+        else if (KBYTES == 16) { u4 x = bld128(rkc, off); R.k[0] = x[0]; R.k[1] = x[1]; R.k[2] = x[2]; R.k[3] = x[3]; }
+        else if (KBYTES == 8) { u2 x = bld64(rkc, off); R.k[0] = x[0]; R.k[1] = x[1]; }
+        else if (KBYTES == 6) {  // 3-bit, D=64: 6 bytes at a 2-byte-aligned offset
+            const uint32_t base = off & ~3u;
+            const int sh = (int)(off - base);
+            u3 x = bld96(rkc, base);
+            R.k[0] = __builtin_amdgcn_alignbyte(x[1], x[0], sh);
+            R.k[1] = __builtin_amdgcn_alignbyte(x[2], x[1], sh) & 0xFFFFu;
+        } else if (KBYTES == 4) { R.k[0] = bld32(rkc, off); }
+        else if (KBYTES == 32) {
+            u4 x = bld128(rkc, off), y = bld128(rkc, off + 16);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { R.k[q] = x[q]; R.k[(4 + q) % WarmRaw<D, KB, VB, WK>::KDW] = y[q]; }
+        }
+    }
+    // V codes: chunk col of tokens t0+4*grp .. +3
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+        const uint32_t rowoff = (uint32_t)(t0 + 4 * grp + jj) * (uint32_t)p.vc_row;
+        uint32_t a = 0u, bb = 0u;
+        if (col < VCH) {
+            if (VB == 4) a = bld32(rvc, rowoff + 4 * col);
+            else if (VB == 2) a = bld16(rvc, rowoff + 2 * col);
+            else if (VB == 8) { u2 x = bld64(rvc, rowoff + 8 * col); a = x[0]; bb = x[1]; }
+            else {  // 3 bytes at 3*col: read the aligned 8 bytes around them
+                const int off = (3 * col) & ~3;
+                u2 x = bld64(rvc, rowoff + off);
+                a = __builtin_amdgcn_alignbyte(x[1], x[0], 3 * col - off);
+            }
+        }
+        R.v[jj][0] = a;
+        if (VB == 8) R.v[jj][VB == 8 ? 1 : 0] = bb;
+    }
+    // V scale/zero of the tile's 16 tokens x ngr groups (staged through LDS at compute time)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        R.ms[i] = 0u;
+        R.mz[i] = 0u;
+        if (e < 16 * ngr) {
+            const int tt = e / ngr, gg = e - tt * ngr;
+            const uint32_t mi = (uint32_t)(t0 + tt) * (uint32_t)ngr + gg;
+            if (WK == AKV_WARM_AFFINE) {
+                R.ms[i] = bld16(rvs, 2 * mi);
+                R.mz[i] = bld16(rvz, 2 * mi);
+            } else {
+                const int tv = min(t0 + tt, nwarm - 1);
+                const int64_t gi = (hw * p.n_warm + tv) * ngr + gg;
+                R.ms[i] = __builtin_bit_cast(uint32_t, load_as_f32(p.vs, gi, p.meta_dt));
+                R.mz[i] = __builtin_bit_cast(uint32_t, load_as_f32(p.vz, gi, p.meta_dt));
+            }
+        }
+    }
+    if (WK == AKV_WARM_LEGACY) {  // K meta of this lane's token (groups covering its channels)
+        const int ng = LCH / p.gs > 0 ? LCH / p.gs : 1;
+        const int64_t mrow = hw * p.n_warm + min(t0 + col, nwarm - 1);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            R.lks[q] = 0.f;
+            R.lkz[q] = 0.f;
+            if (q < ng) {
+                const int gi = (LCH * grp) / p.gs + q;
+                R.lks[q] = load_as_f32(p.ks, mrow * p.lg + gi, p.meta_dt);
+                R.lkz[q] = load_as_f32(p.kz, mrow * p.lg + gi, p.meta_dt);
+            }
+        }
+    }
+}
+
+// Occupancy target of the split kernel (waves per SIMD) handed to the register
+// allocator; 0 leaves the choice to the compiler.
+#ifndef AKV_SPLIT_WAVES_PER_EU
+#define AKV_SPLIT_WAVES_PER_EU 0
+#endif
+#if AKV_SPLIT_WAVES_PER_EU > 0
+#define AKV_SPLIT_ATTR __attribute__((amdgpu_waves_per_eu(AKV_SPLIT_WAVES_PER_EU, AKV_SPLIT_WAVES_PER_EU)))
+#else
+#define AKV_SPLIT_ATTR
+#endif
+
+template <int D, int KB, int VB, int WK, bool OUTL>
+__global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const DecodeParams p) {
+    constexpr int KSTEPS = D / 32, LCH = D / 4, NPAIRS = LCH / 2, VCH = D / 8;
+    using Raw = WarmRaw<D, KB, VB, WK>;
 
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -118,22 +277,20 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     const int nrows = min(16, p.R - row0);
     const bool is_warm = split < p.n_wsplit;
 
-    // this lane's query row (as the N column of the MFMA tiles)
     const int r = row0 + col;
     const int row_valid = col < nrows;
-    const int hq = kvh * p.g + (row_valid ? r / p.M : 0);
-    const int mq = row_valid ? r % p.M : 0;
+    const int rc = row_valid ? r : row0;  // invalid rows reuse a valid query (results discarded)
+    const int hq = kvh * p.g + rc / p.M, mq = rc % p.M;
+    const int64_t strow = ((int64_t)(b * p.Hq + hq) * p.M + mq) * p.N;  // stash row base
 
-    // segment-local token range of this split
-    int64_t t_begin, t_end;
+    int t_begin, t_end;
     if (is_warm) {
-        t_begin = (int64_t)split * p.wsplit_len;
-        t_end = min(t_begin + p.wsplit_len, p.n_warm);
+        t_begin = split * (int)p.wsplit_len;
+        t_end = min(t_begin + (int)p.wsplit_len, (int)p.n_warm);
     } else {
-        t_begin = (int64_t)(split - p.n_wsplit) * p.hsplit_len;
-        t_end = min(t_begin + p.hsplit_len, p.n_hot);
+        t_begin = (split - p.n_wsplit) * (int)p.hsplit_len;
+        t_end = min(t_begin + (int)p.hsplit_len, (int)p.n_hot);
     }
-    // logical index of segment token 0
     const int64_t seg_base = is_warm ? (p.hot_first ? p.n_hot : 0) : (p.hot_first ? 0 : p.n_warm);
 
     // ---- Q operand (B of the QK MFMA): lane = (row col, channel group grp)
@@ -145,22 +302,21 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int pi = 4 * st + j / 2, hf = j % 2;
-                int ch;
-                if (!is_warm) ch = kpair_chan<16>(pi, hf);
-                else ch = kpair_chan<KB>(pi, hf);
-                qop[st][j] = row_valid ? qrow[ch] : (_Float16)0.0f;
+                const int ch = is_warm ? kpair_chan<KB>(pi, hf) : kpair_chan<16>(pi, hf);
+                qop[st][j] = qrow[ch];
             }
     }
 
-    WaveState<D> stt;
-    stt.m = -INFINITY;
+    WaveState stt;
+    stt.m2 = -INFINITY;
     stt.l = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) stt.acc[j] = (f4){0.f, 0.f, 0.f, 0.f};
 
-    unsigned char *wlds = smem + wave * WaveLds<D>::BYTES;
-    uint32_t *kmeta_lds = (uint32_t *)wlds;                          // [2][4][NPAIRS]
-    unsigned char *vmeta_lds = wlds + WaveLds<D>::KMETA;            // [2][ng][16]
+    // per-wave LDS staging: K meta [s'|s|z][4 grp][16 pairs] u32 (768 B),
+    // V meta [s|z][16 groups][16 tokens] of <= 4 B (2 KiB)
+    uint32_t *kmeta_lds = (uint32_t *)(smem + wave * 2816);
+    unsigned char *vmeta_lds = smem + wave * 2816 + 768;
 
     const int64_t bh = (int64_t)b * p.Hkv + kvh;
     const float sl2 = p.scale_log2;
@@ -169,260 +325,303 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
         // ------------------------------------------------------------ hot tiles
         const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.khot + bh * p.n_hot * D, (uint32_t)(p.n_hot * D * 2));
         const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vhot + bh * p.n_hot * D, (uint32_t)(p.n_hot * D * 2));
-        for (int64_t t0 = t_begin + 16 * wave; t0 < t_end; t0 += 16 * NW) {
-            // K: lane's token t0+col, channels LCH*grp .. +LCH (fp16, natural order)
-            const int64_t tk = t0 + col;
+        for (int t0 = t_begin + 16 * wave; t0 < t_end; t0 += 16 * kNW) {
             h8 kop[KSTEPS];
 #pragma unroll
             for (int st = 0; st < KSTEPS; ++st) {
-                u4 raw = bld128(rk, (uint32_t)((tk * D + LCH * grp + 8 * st) * 2));
+                u4 raw = bld128(rk, (uint32_t)(((t0 + col) * D + LCH * grp + 8 * st) * 2));
                 kop[st] = __builtin_bit_cast(h8, raw);
             }
+            u4 w[4];
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj)
+                w[jj] = (col < VCH) ? bld128(rv, (uint32_t)(((t0 + 4 * grp + jj) * D + 8 * col) * 2))
+                                    : (u4){0u, 0u, 0u, 0u};
             f4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int st = 0; st < KSTEPS; ++st) s = mfma_k32(kop[st], qop[st], s);
-            bool valid[4];
+            const int nvalid = min(4, t_end - (t0 + 4 * grp));
+            if (t0 + 16 > t_end) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                valid[i] = (t0 + 4 * grp + i) < t_end;
-                s[i] = valid[i] ? s[i] * sl2 : -INFINITY;
+                for (int i = 0; i < 4; ++i)
+                    if (i >= nvalid) s[i] = -INFINITY;
             }
-            store_stash<D>(p, b, row_valid, hq, mq, seg_base + t0 + 4 * grp, s, valid);
-            // V: lane's chunk col (8 channels), tokens t0+4*grp .. +3
-            h4 vop[8];
-            {
-                u4 w[4];
+            store_stash(p, strow, row_valid, seg_base + t0 + 4 * grp, s, sl2, nvalid);
+            const h4 pop = softmax_tile(stt, s, sl2);
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const int64_t tv = t0 + 4 * grp + jj;
-                    w[jj] = (col < VCH && tv < t_end) ? bld128(rv, (uint32_t)((tv * D + 8 * col) * 2))
-                                                      : (u4){0u, 0u, 0u, 0u};
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-                    const uint32_t lo = perm(w[1][j / 2], w[0][j / 2], sel);
-                    const uint32_t hi = perm(w[3][j / 2], w[2][j / 2], sel);
-                    vop[j] = __builtin_bit_cast(h4, (u2){lo, hi});
-                }
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t lo = perm(w[1][j / 2], w[0][j / 2], sel);
+                const uint32_t hi = perm(w[3][j / 2], w[2][j / 2], sel);
+                stt.acc[j] = mfma_k16(__builtin_bit_cast(h4, (u2){lo, hi}), pop, stt.acc[j]);
             }
-            softmax_pv<D>(stt, s, vop);
         }
     } else {
         // ----------------------------------------------------------- warm tiles
         const int unit = (WK == AKV_WARM_AFFINE) ? p.T : 16;  // tokens sharing K meta
         const int64_t hw = (WK == AKV_WARM_AFFINE) ? bh : (p.warm_heads == 1 ? 0 : kvh);
+        const int nwarm = (int)p.n_warm;
         const __amdgpu_buffer_rsrc_t rkc =
             make_rsrc((const unsigned char *)p.kc + hw * p.n_warm * p.kc_row, (uint32_t)(p.n_warm * p.kc_row));
         const __amdgpu_buffer_rsrc_t rvc =
             make_rsrc((const unsigned char *)p.vc + hw * p.n_warm * p.vc_row, (uint32_t)(p.n_warm * p.vc_row));
+        const int ngr = (WK == AKV_WARM_AFFINE) ? D / p.Gv : p.lg;
+        const __amdgpu_buffer_rsrc_t rvs =
+            make_rsrc((const _Float16 *)p.vs + hw * p.n_warm * ngr, (uint32_t)(p.n_warm * ngr * 2));
+        const __amdgpu_buffer_rsrc_t rvz =
+            make_rsrc((const _Float16 *)p.vz + hw * p.n_warm * ngr, (uint32_t)(p.n_warm * ngr * 2));
+        const __amdgpu_buffer_rsrc_t rks =
+            make_rsrc((const _Float16 *)p.ks + bh * p.nblk * D, (uint32_t)(p.nblk * D * 2));
+        const __amdgpu_buffer_rsrc_t rkz =
+            make_rsrc((const _Float16 *)p.kz + bh * p.nblk * D, (uint32_t)(p.nblk * D * 2));
         int ksym = 0, vsym = 0;
         if (WK == AKV_WARM_LEGACY) {
             ksym = p.sym_flags ? p.sym_flags[0] : p.legacy_sym;
             vsym = p.sym_flags ? p.sym_flags[1] : p.legacy_sym;
         }
-        for (int64_t u0 = t_begin + (int64_t)unit * wave; u0 < t_end; u0 += (int64_t)unit * NW) {
-            // ---- K meta for this unit -> LDS in pair order (affine: per channel of the block)
-            if (WK == AKV_WARM_AFFINE) {
-                const int64_t blk = u0 / p.T;
-                const _Float16 *ks = (const _Float16 *)p.ks + (bh * p.nblk + blk) * D;
-                const _Float16 *kz = (const _Float16 *)p.kz + (bh * p.nblk + blk) * D;
-                // lane -> (grp' = lane/16, pair = lane%16); pairs >= NPAIRS unused for D=64
-                const int g2 = lane >> 4, pi = lane & 15;
-                if (pi < NPAIRS) {
-                    int clo = 0, chi = 0;
+        const int gsz = (WK == AKV_WARM_AFFINE) ? p.Gv : p.gs;
+        const int gme = min((8 * col) / gsz, 15);  // V group of this lane's chunk
+        // K meta staging role of this lane: (group g2, pair pi2)
+        const int g2 = lane >> 4, pi2 = lane & 15;
+        int clo = 0, chi = 0, ko2 = 0;
 #pragma unroll
-                    for (int q = 0; q < NPAIRS; ++q)
-                        if (q == pi) { clo = kpair_chan<KB>(q, 0); chi = kpair_chan<KB>(q, 1); }
-                    const int base = LCH * g2;
-                    h2 sv = {ks[base + clo], ks[base + chi]};
-                    h2 zv = {kz[base + clo], kz[base + chi]};
-                    kmeta_lds[(0 * 4 + g2) * NPAIRS + pi] = as_u32(sv);
-                    kmeta_lds[(1 * 4 + g2) * NPAIRS + pi] = as_u32(zv);
+        for (int q = 0; q < NPAIRS; ++q)
+            if (q == pi2) { clo = kpair_chan<KB>(q, 0); chi = kpair_chan<KB>(q, 1); ko2 = koff<KB>(q); }
+        const uint32_t kmo_lo = (uint32_t)(LCH * g2 + clo) * 2, kmo_hi = (uint32_t)(LCH * g2 + chi) * 2;
+
+        Raw cur, nxt;
+        uint32_t km_s = 0u, km_z = 0u;  // prefetched K meta pair (s, z) of the next unit (affine)
+        int u0 = t_begin + unit * wave;
+        if (u0 < t_end) {
+            load_warm_tile<D, KB, VB, WK>(nxt, p, u0, lane, col, grp, rkc, rvc, rvs, rvz, ngr, nwarm, hw);
+            if (WK == AKV_WARM_AFFINE && pi2 < NPAIRS) {
+                const uint32_t mo = (uint32_t)(u0 / p.T) * D * 2;
+                km_s = (uint32_t)bld16(rks, mo + kmo_lo) | ((uint32_t)bld16(rks, mo + kmo_hi) << 16);
+                km_z = (uint32_t)bld16(rkz, mo + kmo_lo) | ((uint32_t)bld16(rkz, mo + kmo_hi) << 16);
+            }
+        }
+        for (; u0 < t_end; u0 += unit * kNW) {
+            // ---- K meta of this unit -> LDS (affine: per channel of the block, pair order)
+            bool fast = true;
+            if (WK == AKV_WARM_AFFINE) {
+                if (pi2 < NPAIRS) {
+                    const h2 sv = as_h2(km_s);
+                    const _Float16 f = (_Float16)(1.0f / (float)(1 << ko2));
+                    const h2 sp = sv * (h2){f, f};
+                    const _Float16 gm = (_Float16)(float)(1 << ko2);
+                    const h2 back = sp * (h2){gm, gm};
+                    fast = (back[0] == sv[0]) && (back[1] == sv[1]);
+                    kmeta_lds[(0 * 4 + g2) * 16 + pi2] = as_u32(sp);
+                    kmeta_lds[(1 * 4 + g2) * 16 + pi2] = km_s;
+                    kmeta_lds[(2 * 4 + g2) * 16 + pi2] = km_z;
+                }
+                fast = !__builtin_amdgcn_ballot_w64(!fast);
+                const int nu = u0 + unit * kNW;
+                if (nu < t_end && pi2 < NPAIRS) {  // prefetch the next unit's K meta
+                    const uint32_t mo = (uint32_t)(nu / p.T) * D * 2;
+                    km_s = (uint32_t)bld16(rks, mo + kmo_lo) | ((uint32_t)bld16(rks, mo + kmo_hi) << 16);
+                    km_z = (uint32_t)bld16(rkz, mo + kmo_lo) | ((uint32_t)bld16(rkz, mo + kmo_hi) << 16);
                 }
                 __builtin_amdgcn_wave_barrier();
             }
-            const int64_t u1 = min(u0 + unit, t_end);
-            for (int64_t t0 = u0; t0 < u1; t0 += 16) {
-                // ---- K codes: lane's token t0+col, channels LCH*grp..+LCH
-                const int64_t tk = t0 + col;
-                uint32_t kr[4] = {0u, 0u, 0u, 0u};
-                uint32_t kr8[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-                {
-                    const uint32_t off = (uint32_t)(tk * p.kc_row + KBYTES * grp);
-                    if (KB == 8) {
+            h2 ksc[NPAIRS], kze[NPAIRS];
+            if (WK == AKV_WARM_AFFINE) {
+                const uint32_t *src_s = kmeta_lds + ((fast ? 0 : 1) * 4 + grp) * 16;
 #pragma unroll
-                        for (int q = 0; q < KDW; q += 4) {
-                            u4 x = bld128(rkc, off + 4 * q);
-                            kr8[q] = x[0]; kr8[q + 1] = x[1]; kr8[q + 2] = x[2]; kr8[q + 3] = x[3];
-                        }
-                    } else if (KBYTES == 12) { u3 x = bld96(rkc, off); kr[0] = x[0]; kr[1] = x[1]; kr[2] = x[2]; }
-                    else if (KBYTES == 16) { u4 x = bld128(rkc, off); kr[0] = x[0]; kr[1] = x[1]; kr[2] = x[2]; kr[3] = x[3]; }
-                    else if (KBYTES == 8) { u2 x = bld64(rkc, off); kr[0] = x[0]; kr[1] = x[1]; }
-                    else if (KBYTES == 6) {  // 3-bit, D=64: 6 bytes at a 2-byte-aligned offset
-                        const uint32_t base = off & ~3u;
-                        const int sh = (int)(off - base);
-                        u3 x = bld96(rkc, base);
-                        kr[0] = __builtin_amdgcn_alignbyte(x[1], x[0], sh);
-                        kr[1] = __builtin_amdgcn_alignbyte(x[2], x[1], sh) & 0xFFFFu;
-                    }
-                    else if (KBYTES == 4) { kr[0] = bld32(rkc, off); }
+                for (int q = 0; q < NPAIRS; ++q) {
+                    ksc[q] = as_h2(src_s[q]);
+                    kze[q] = as_h2(kmeta_lds[(2 * 4 + grp) * 16 + q]);
                 }
-                // ---- K meta for this tile
-                h2 ksc[NPAIRS], kze[NPAIRS];
-                if (WK == AKV_WARM_AFFINE) {
-#pragma unroll
-                    for (int q = 0; q < NPAIRS; ++q) {
-                        ksc[q] = as_h2(kmeta_lds[(0 * 4 + grp) * NPAIRS + q]);
-                        kze[q] = as_h2(kmeta_lds[(1 * 4 + grp) * NPAIRS + q]);
-                    }
+            }
+            const int u1 = min(u0 + unit, t_end);
+            for (int t0 = u0; t0 < u1; t0 += 16) {
+                cur = nxt;
+                {  // prefetch the next tile of this wave
+                    int tn = t0 + 16;
+                    if (tn >= u1) tn = u0 + unit * kNW;
+                    if (tn < t_end)
+                        load_warm_tile<D, KB, VB, WK>(nxt, p, tn, lane, col, grp, rkc, rvc, rvs, rvz, ngr, nwarm, hw);
                 }
-                float lks[4] = {0.f, 0.f, 0.f, 0.f}, lkz[4] = {0.f, 0.f, 0.f, 0.f};
-                if (WK == AKV_WARM_LEGACY) {
-                    // groups covering channels LCH*grp .. +LCH (gs >= 8, power of two)
-                    const int ng = LCH / p.gs > 0 ? LCH / p.gs : 1;
-                    const int64_t mrow = hw * p.n_warm + min(tk, p.n_warm - 1);
+                // ---- V meta of the tile -> LDS [s|z][group][token]
 #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        if (q < ng) {
-                            const int gi = (LCH * grp) / p.gs + q;
-                            lks[q] = load_as_f32(p.ks, mrow * p.lg + gi, p.meta_dt);
-                            lkz[q] = load_as_f32(p.kz, mrow * p.lg + gi, p.meta_dt);
-                        }
-                }
-                // ---- dequant + QK
-                f4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int st = 0; st < KSTEPS; ++st) {
-                    h8 a;
-#pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int pi = 4 * st + k;
-                        const uint32_t cp = (KB == 8) ? kpair_extract<8>(kr8, pi) : kpair_extract<KB>(kr, pi);
-                        h2 v;
+                for (int i = 0; i < 4; ++i) {
+                    const int e = lane + 64 * i;
+                    if (e < 16 * ngr) {
+                        const int tt = e / ngr, gg = e - tt * ngr;
                         if (WK == AKV_WARM_AFFINE) {
-                            v = deq_affine(cp, ksc[pi], kze[pi]);
+                            ((uint16_t *)vmeta_lds)[(0 * 16 + gg) * 16 + tt] = (uint16_t)cur.ms[i];
+                            ((uint16_t *)vmeta_lds)[(1 * 16 + gg) * 16 + tt] = (uint16_t)cur.mz[i];
                         } else {
+                            ((uint32_t *)vmeta_lds)[(0 * 16 + gg) * 16 + tt] = cur.ms[i];
+                            ((uint32_t *)vmeta_lds)[(1 * 16 + gg) * 16 + tt] = cur.mz[i];
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                h2 vs01, vs23, vz01, vz23;
+                float fvs[4], fvz[4];
+                if (WK == AKV_WARM_AFFINE) {
+                    const u2 sp = *(const u2 *)((const uint16_t *)vmeta_lds + (0 * 16 + gme) * 16 + 4 * grp);
+                    const u2 zp = *(const u2 *)((const uint16_t *)vmeta_lds + (1 * 16 + gme) * 16 + 4 * grp);
+                    vs01 = as_h2(sp[0]); vs23 = as_h2(sp[1]);
+                    vz01 = as_h2(zp[0]); vz23 = as_h2(zp[1]);
+                } else {
+                    const u4 sp = *(const u4 *)((const uint32_t *)vmeta_lds + (0 * 16 + gme) * 16 + 4 * grp);
+                    const u4 zp = *(const u4 *)((const uint32_t *)vmeta_lds + (1 * 16 + gme) * 16 + 4 * grp);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        // copy the element out first: bit-casting a subscripted
+                        // ext-vector lvalue reads element 0 whatever the index
+                        const uint32_t ws = sp[i], wz = zp[i];
+                        fvs[i] = __builtin_bit_cast(float, ws);
+                        fvz[i] = __builtin_bit_cast(float, wz);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+
+                // ---- K dequant + QK
+                f4 s = {0.f, 0.f, 0.f, 0.f};
+                if (WK == AKV_WARM_AFFINE && KB != 8) {
+                    KWin<KB> W;
+                    k_windows<KB, NPAIRS>(cur.k, W);
+                    const h2 magic = {(_Float16)1024.0f, (_Float16)1024.0f};
+                    if (fast) {
+                        // the code stays 2^o above bit 0; the scale was divided by 2^o
+#pragma unroll
+                        for (int st = 0; st < KSTEPS; ++st) {
+                            h8 a;
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const int pi = 4 * st + k;
+                                const h2 c = as_h2(and_or(k_window_of<KB>(W, pi), kmask<KB>(pi), kMagic)) - magic;
+                                h2 v = c * ksc[pi];
+                                v = v + kze[pi];
+                                a[2 * k] = v[0];
+                                a[2 * k + 1] = v[1];
+                            }
+                            s = mfma_k32(a, qop[st], s);
+                        }
+                    } else {
+#pragma unroll
+                        for (int st = 0; st < KSTEPS; ++st) {
+                            h8 a;
+#pragma unroll
+                            for (int k = 0; k < 4; ++k) {
+                                const int pi = 4 * st + k;
+                                const uint32_t z = k_window_of<KB>(W, pi) >> koff<KB>(pi);
+                                const h2 c = as_h2(and_or(z, kmask<KB>(0), kMagic)) - magic;
+                                h2 v = c * ksc[pi];
+                                v = v + kze[pi];
+                                a[2 * k] = v[0];
+                                a[2 * k + 1] = v[1];
+                            }
+                            s = mfma_k32(a, qop[st], s);
+                        }
+                    }
+                } else {
+#pragma unroll
+                    for (int st = 0; st < KSTEPS; ++st) {
+                        h8 a;
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) {
+                            const int pi = 4 * st + k;
+                            const uint32_t cp = kpair_extract<KB>(cur.k, pi);
                             const int c0 = kpair_chan<KB>(pi, 0), c1 = kpair_chan<KB>(pi, 1);
                             const int q0 = (LCH / p.gs > 0) ? c0 / p.gs : 0;
                             const int q1 = (LCH / p.gs > 0) ? c1 / p.gs : 0;
-                            const float s0 = q0 == 0 ? lks[0] : q0 == 1 ? lks[1] : q0 == 2 ? lks[2] : lks[3];
-                            const float s1 = q1 == 0 ? lks[0] : q1 == 1 ? lks[1] : q1 == 2 ? lks[2] : lks[3];
-                            const float z0 = q0 == 0 ? lkz[0] : q0 == 1 ? lkz[1] : q0 == 2 ? lkz[2] : lkz[3];
-                            const float z1 = q1 == 0 ? lkz[0] : q1 == 1 ? lkz[1] : q1 == 2 ? lkz[2] : lkz[3];
+                            const float s0 = q0 == 0 ? cur.lks[0] : q0 == 1 ? cur.lks[1] : q0 == 2 ? cur.lks[2] : cur.lks[3];
+                            const float s1 = q1 == 0 ? cur.lks[0] : q1 == 1 ? cur.lks[1] : q1 == 2 ? cur.lks[2] : cur.lks[3];
+                            const float z0 = q0 == 0 ? cur.lkz[0] : q0 == 1 ? cur.lkz[1] : q0 == 2 ? cur.lkz[2] : cur.lkz[3];
+                            const float z1 = q1 == 0 ? cur.lkz[0] : q1 == 1 ? cur.lkz[1] : q1 == 2 ? cur.lkz[2] : cur.lkz[3];
                             const float u0f = (float)(cp & 0xFFFFu), u1f = (float)(cp >> 16);
                             float d0, d1;
                             if (ksym) { d0 = (u0f - p.half_max_k) * s0; d1 = (u1f - p.half_max_k) * s1; }
                             else { d0 = u0f * s0; d0 = d0 + z0; d1 = u1f * s1; d1 = d1 + z1; }
-                            v = (h2){(_Float16)d0, (_Float16)d1};
+                            a[2 * k] = (_Float16)d0;
+                            a[2 * k + 1] = (_Float16)d1;
                         }
-                        a[2 * k] = v[0];
-                        a[2 * k + 1] = v[1];
+                        s = mfma_k32(a, qop[st], s);
                     }
-                    s = mfma_k32(a, qop[st], s);
                 }
-                bool valid[4];
+                const int nvalid = min(4, t_end - (t0 + 4 * grp));
+                if (t0 + 16 > t_end) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    valid[i] = (t0 + 4 * grp + i) < t_end;
-                    s[i] = valid[i] ? s[i] * sl2 : -INFINITY;
+                    for (int i = 0; i < 4; ++i)
+                        if (i >= nvalid) s[i] = -INFINITY;
                 }
-                // ---- K outlier channels (affine): replace the dequantized value of
-                // channel d_j by the stored fp16 value -> add q[d_j]*(o - kdeq) to s
-                if (WK == AKV_WARM_AFFINE && p.n_out > 0) {
+                // ---- K outlier channels (affine): the stored fp16 value replaces the
+                // dequantized one -> add q[d_j] * (o - kdeq) to the raw dot product
+                if (OUTL) {
                     const int64_t blk = t0 / p.T;
 #pragma unroll 1
                     for (int j = 0; j < p.n_out; ++j) {
                         const int dj = min(max((int)p.k_oidx[((int64_t)b * p.nblk + blk) * p.n_out + j], 0), D - 1);
-                        const float qd = row_valid ? (float)p.q[((int64_t)(b * p.Hq + hq) * p.M + mq) * D + dj] : 0.f;
+                        const float qd = (float)p.q[((int64_t)(b * p.Hq + hq) * p.M + mq) * D + dj];
                         const _Float16 ksj = ((const _Float16 *)p.ks)[(bh * p.nblk + blk) * D + dj];
                         const _Float16 kzj = ((const _Float16 *)p.kz)[(bh * p.nblk + blk) * D + dj];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
-                            if (!valid[i]) continue;
+                            if (i >= nvalid) continue;
                             const int64_t t = t0 + 4 * grp + i;
                             const unsigned char *row = (const unsigned char *)p.kc + (hw * p.n_warm + t) * p.kc_row;
                             const uint32_t code = extract_code(row, dj, KB);
                             const _Float16 kd = (_Float16)((_Float16)((_Float16)code * ksj) + kzj);
                             const _Float16 od = ((const _Float16 *)p.k_odata)[(bh * p.n_warm + t) * p.n_out + j];
-                            s[i] += qd * ((float)od - (float)kd) * sl2;
+                            s[i] += qd * ((float)od - (float)kd);
                         }
                     }
                 }
-                store_stash<D>(p, b, row_valid, hq, mq, seg_base + t0 + 4 * grp, s, valid);
+                store_stash(p, strow, row_valid, seg_base + t0 + 4 * grp, s, sl2, nvalid);
 
-                // ---- V: lane's chunk col, tokens t0+4*grp .. +3
-                uint32_t wv[4][2];
-                {
-                    constexpr int CB = VB;  // bytes per 8-channel chunk
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const int64_t tv = t0 + 4 * grp + jj;
-                        wv[jj][0] = 0u; wv[jj][1] = 0u;
-                        if (col < VCH) {
-                            const uint32_t rowoff = (uint32_t)(tv * p.vc_row);
-                            if (VB == 4) wv[jj][0] = bld32(rvc, rowoff + 4 * col);
-                            else if (VB == 2) wv[jj][0] = bld16(rvc, rowoff + 2 * col);
-                            else if (VB == 8) { u2 x = bld64(rvc, rowoff + 8 * col); wv[jj][0] = x[0]; wv[jj][1] = x[1]; }
-                            else {  // 3-bit: 3 bytes at 3*col, read the aligned 8 bytes around them
-                                const int off = (3 * col) & ~3;
-                                const int sh = 3 * col - off;
-                                u2 x = bld64(rvc, rowoff + off);
-                                wv[jj][0] = __builtin_amdgcn_alignbyte(x[1], x[0], sh);
-                            }
-                        }
-                        (void)CB;
+                const h4 pop = softmax_tile(stt, s, sl2);
+                // ---- V dequant (4 tokens x 8 channels of chunk col) + PV per channel slot
+                int vo_dj[2] = {-1, -1};  // outlier channels of this block in this lane's chunk (first two)
+                if (OUTL) {
+                    const int64_t blk = t0 / p.T;
+                    int cnt = 0;
+#pragma unroll 1
+                    for (int j = 0; j < p.n_out && cnt < 2; ++j) {
+                        const int dj = min(max((int)p.v_oidx[((int64_t)b * p.nblk + blk) * p.n_out + j], 0), D - 1);
+                        if (dj / 8 == col) vo_dj[cnt++] = j;
                     }
                 }
-                // V meta: per token of the tile, for the group of chunk col -> LDS [s|z][group][token]
-                h2 vs01 = {}, vs23 = {}, vz01 = {}, vz23 = {};
-                float fvs[4] = {0.f, 0.f, 0.f, 0.f}, fvz[4] = {0.f, 0.f, 0.f, 0.f};
-                {
-                    const int ngr = (WK == AKV_WARM_AFFINE) ? D / p.Gv : p.lg;
-                    const int tot = 16 * ngr;  // <= 16*16
-                    for (int e = lane; e < tot; e += 64) {
-                        const int tt = e / ngr, gg = e % ngr;
-                        const int64_t tv = min(t0 + tt, p.n_warm - 1);
-                        if (WK == AKV_WARM_AFFINE) {
-                            const int64_t mi = (bh * p.n_warm + tv) * ngr + gg;
-                            ((_Float16 *)vmeta_lds)[(0 * 16 + gg) * 16 + tt] = ((const _Float16 *)p.vs)[mi];
-                            ((_Float16 *)vmeta_lds)[(1 * 16 + gg) * 16 + tt] = ((const _Float16 *)p.vz)[mi];
-                        } else {
-                            const int64_t mi = (hw * p.n_warm + tv) * ngr + gg;
-                            ((float *)vmeta_lds)[(0 * 16 + gg) * 16 + tt] = load_as_f32(p.vs, mi, p.meta_dt);
-                            ((float *)vmeta_lds)[(1 * 16 + gg) * 16 + tt] = load_as_f32(p.vz, mi, p.meta_dt);
-                        }
-                    }
-                    __builtin_amdgcn_wave_barrier();
-                    const int gsz = (WK == AKV_WARM_AFFINE) ? p.Gv : p.gs;
-                    const int gme = min((8 * col) / gsz, 15);
-                    if (WK == AKV_WARM_AFFINE) {
-                        const uint32_t *sp = (const uint32_t *)vmeta_lds + ((0 * 16 + gme) * 16 + 4 * grp) / 2;
-                        const uint32_t *zp = (const uint32_t *)vmeta_lds + ((1 * 16 + gme) * 16 + 4 * grp) / 2;
-                        vs01 = as_h2(sp[0]); vs23 = as_h2(sp[1]);
-                        vz01 = as_h2(zp[0]); vz23 = as_h2(zp[1]);
-                    } else {
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            fvs[i] = ((const float *)vmeta_lds)[(0 * 16 + gme) * 16 + 4 * grp + i];
-                            fvz[i] = ((const float *)vmeta_lds)[(1 * 16 + gme) * 16 + 4 * grp + i];
-                        }
-                    }
-                    __builtin_amdgcn_wave_barrier();
-                }
-                h4 vop[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const uint32_t c01 = vpair_extract<VB>(wv[0], wv[1], j);
-                    const uint32_t c23 = vpair_extract<VB>(wv[2], wv[3], j);
+                    uint32_t c01, c23;
+                    if (VB == 3) {
+                        const uint32_t sel = j < 5 ? 0x05060102u : 0x04050001u;
+                        const int sh = j < 5 ? 3 * j : 7 + 3 * (j - 5);
+                        c01 = perm(cur.v[1][0], cur.v[0][0], sel) >> sh;
+                        c23 = perm(cur.v[3][0], cur.v[2][0], sel) >> sh;
+                    } else if (VB == 4) {
+                        const uint32_t sel = j < 4 ? 0x05040100u : 0x07060302u;
+                        c01 = perm(cur.v[1][0], cur.v[0][0], sel) >> (4 * (j & 3));
+                        c23 = perm(cur.v[3][0], cur.v[2][0], sel) >> (4 * (j & 3));
+                    } else if (VB == 2) {
+                        c01 = ((cur.v[0][0] & 0xFFFFu) | (cur.v[1][0] << 16)) >> (2 * j);
+                        c23 = ((cur.v[2][0] & 0xFFFFu) | (cur.v[3][0] << 16)) >> (2 * j);
+                    } else {  // 8-bit: byte j%4 of dword j/4
+                        constexpr int VW = (VB == 8) ? 2 : 1;
+                        const int dw = (j / 4) % VW;
+                        const uint32_t sel = (uint32_t)((j & 3) | (0x0C << 8) | ((4 + (j & 3)) << 16) | (0x0C << 24));
+                        c01 = perm(cur.v[1][dw], cur.v[0][dw], sel);
+                        c23 = perm(cur.v[3][dw], cur.v[2][dw], sel);
+                    }
+                    const uint32_t vm =
+                        (VB == 3) ? 0x00070007u : (VB == 4 ? 0x000F000Fu : (VB == 2 ? 0x00030003u : 0x00FF00FFu));
+                    c01 = and_or(c01, vm, kMagic);
+                    c23 = and_or(c23, vm, kMagic);
+                    const h2 magic = {(_Float16)1024.0f, (_Float16)1024.0f};
                     h2 a01, a23;
                     if (WK == AKV_WARM_AFFINE) {
-                        a01 = deq_affine(c01, vs01, vz01);
-                        a23 = deq_affine(c23, vs23, vz23);
+                        a01 = (as_h2(c01) - magic) * vs01;
+                        a01 = a01 + vz01;
+                        a23 = (as_h2(c23) - magic) * vs23;
+                        a23 = a23 + vz23;
                     } else {
+                        const h2 x01 = as_h2(c01) - magic, x23 = as_h2(c23) - magic;
+                        const float u[4] = {(float)x01[0], (float)x01[1], (float)x23[0], (float)x23[1]};
                         float d[4];
-                        const float u[4] = {(float)(c01 & 0xFFFFu), (float)(c01 >> 16), (float)(c23 & 0xFFFFu),
-                                            (float)(c23 >> 16)};
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
                             if (vsym) d[i] = (u[i] - p.half_max_v) * fvs[i];
@@ -431,28 +630,23 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
                         a01 = (h2){(_Float16)d[0], (_Float16)d[1]};
                         a23 = (h2){(_Float16)d[2], (_Float16)d[3]};
                     }
-                    vop[j] = (h4){a01[0], a01[1], a23[0], a23[1]};
-                }
-                // V outliers: the chunk holding d_j gets the stored value (replace)
-                if (WK == AKV_WARM_AFFINE && p.n_out > 0) {
-                    const int64_t blk = t0 / p.T;
-#pragma unroll 1
-                    for (int j = 0; j < p.n_out; ++j) {
-                        const int dj = min(max((int)p.v_oidx[((int64_t)b * p.nblk + blk) * p.n_out + j], 0), D - 1);
-                        if (dj / 8 != col) continue;
-                        const int within = dj % 8;
+                    h4 vop = {a01[0], a01[1], a23[0], a23[1]};
+                    if (OUTL && vo_dj[0] >= 0) {  // rare: outlier channels replace values
 #pragma unroll
-                        for (int jj = 0; jj < 8; ++jj) {
-                            if (vpair_chan<VB>(jj) != within) continue;
+                        for (int q = 0; q < 2; ++q) {
+                            const int jo = vo_dj[q];
+                            if (jo < 0) continue;
+                            const int dj = (int)p.v_oidx[((int64_t)b * p.nblk + t0 / p.T) * p.n_out + jo];
+                            if (vpair_chan<VB>(j) != dj % 8) continue;
 #pragma unroll
                             for (int i = 0; i < 4; ++i) {
-                                const int64_t tv = min(t0 + 4 * grp + i, p.n_warm - 1);
-                                vop[jj][i] = ((const _Float16 *)p.v_odata)[(bh * p.n_warm + tv) * p.n_out + j];
+                                const int64_t tv = min(t0 + 4 * grp + i, nwarm - 1);
+                                vop[i] = ((const _Float16 *)p.v_odata)[(bh * p.n_warm + tv) * p.n_out + jo];
                             }
                         }
                     }
+                    stt.acc[j] = mfma_k16(vop, pop, stt.acc[j]);
                 }
-                softmax_pv<D>(stt, s, vop);
             }
         }
     }
@@ -461,10 +655,10 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     stt.l = wave_sum16(stt.l);
     __syncthreads();
     float *mlds = (float *)smem;                   // [NW][16] max
-    float *llds = mlds + NW * 16;                  // [NW][16] sum
-    float *alds = llds + NW * 16;                  // [NW][16][D] acc
+    float *llds = mlds + kNW * 16;                 // [NW][16] sum
+    float *alds = llds + kNW * 16;                 // [NW][16][D] acc
     if (grp == 0) {
-        mlds[wave * 16 + col] = stt.m;
+        mlds[wave * 16 + col] = stt.m2;
         llds[wave * 16 + col] = stt.l;
     }
     const int vperm_hot = !is_warm;
@@ -484,12 +678,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
         const int rr = e / D, ch = e % D;
         float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, mlds[w * 16 + rr]);
+        for (int w = 0; w < kNW; ++w) mx = fmaxf(mx, mlds[w * 16 + rr]);
         float a = 0.f, l = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
+        for (int w = 0; w < kNW; ++w) {
             const float mw = mlds[w * 16 + rr];
-            const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - mx);
+            const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
             a += f * alds[(w * 16 + rr) * D + ch];
             l += f * llds[w * 16 + rr];
         }
@@ -501,93 +695,116 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const DecodeParams p)
     }
 }
 
-// Merge the split partials of one (batch, kv-head, row chunk): out = sum f_s acc_s / (L * 2^7),
-// f_s = exp2(m_s - M); also records (M, L) per query row for the weights / importance pass.
+// Merge the split partials of one query row: out = sum_s f_s acc_s / sum_s f_s l_s,
+// f_s = exp2(m_s - M).  One workgroup (D threads) per (batch, kv-head, chunk, row).
 template <int D>
-__global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p) {
-    __shared__ float fac[16 * 256];
-    __shared__ float rowM[16], rowL[16];
-    const int bhc = blockIdx.x;
+__global__ __launch_bounds__(D) void decode_reduce_kernel(const DecodeParams p) {
+    __shared__ float fs[1024];
+    __shared__ float red[D / 64][2];
+    const int bhc = blockIdx.x, rr = blockIdx.y;
     const int chunk = bhc % p.nchunk;
     const int64_t bh = bhc / p.nchunk;
     const int b = (int)(bh / p.Hkv), kvh = (int)(bh % p.Hkv);
     const int row0 = chunk * 16, nrows = min(16, p.R - row0);
+    if (rr >= nrows) return;
     const int ns = p.nsplit;
     const int64_t pstride = (int64_t)p.prows * (D + 2);
-    const float *part = p.part + (bh * p.nchunk + chunk) * (int64_t)ns * pstride;
-    if (threadIdx.x < nrows) {
-        const int rr = threadIdx.x;
-        float mx = -INFINITY;
-        for (int s = 0; s < ns; ++s) mx = fmaxf(mx, part[s * pstride + rr * (D + 2)]);
-        float l = 0.f;
-        for (int s = 0; s < ns; ++s) {
-            const float ms = part[s * pstride + rr * (D + 2)];
-            const float f = (ms == -INFINITY) ? 0.f : exp2f(ms - mx);
-            l += f * part[s * pstride + rr * (D + 2) + 1];
-        }
-        rowM[rr] = mx;
-        rowL[rr] = l;
-    }
+    const float *part = p.part + (bh * p.nchunk + chunk) * (int64_t)ns * pstride + rr * (D + 2);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // row max over the splits
+    float mx = -INFINITY;
+    for (int s = tid; s < ns; s += D) mx = fmaxf(mx, part[s * pstride]);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) red[w][0] = mx;
     __syncthreads();
-    const bool fit = ns <= 256;
-    if (fit) {
-        for (int e = threadIdx.x; e < nrows * ns; e += 256) {
-            const int rr = e / ns, s = e % ns;
-            const float ms = part[s * pstride + rr * (D + 2)];
-            fac[rr * 256 + s] = (ms == -INFINITY) ? 0.f : exp2f(ms - rowM[rr]);
-        }
+    mx = red[0][0];
+#pragma unroll
+    for (int i = 1; i < D / 64; ++i) mx = fmaxf(mx, red[i][0]);
+    // split factors and the row sum
+    float l = 0.f;
+    for (int s = tid; s < ns; s += D) {
+        const float ms = part[s * pstride];
+        const float f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+        if (s < 1024) fs[s] = f;
+        l += f * part[s * pstride + 1];
     }
+    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
     __syncthreads();
-    for (int e = threadIdx.x; e < nrows * D; e += 256) {
-        const int rr = e / D, ch = e % D;
-        float a = 0.f;
-        for (int s = 0; s < ns; ++s) {
-            float f;
-            if (fit) f = fac[rr * 256 + s];
-            else {
-                const float ms = part[s * pstride + rr * (D + 2)];
-                f = (ms == -INFINITY) ? 0.f : exp2f(ms - rowM[rr]);
-            }
-            a += f * part[s * pstride + rr * (D + 2) + 2 + ch];
-        }
-        const float o = a / (rowL[rr] * kPScale);
-        const int r = row0 + rr;
-        const int h = kvh * p.g + r / p.M, m = r % p.M;
-        p.out[((int64_t)(b * p.Hq + h) * p.M + m) * D + ch] = (_Float16)o;
+    if (lane == 0) red[w][1] = l;
+    __syncthreads();
+    float L = 0.f;
+#pragma unroll
+    for (int i = 0; i < D / 64; ++i) L += red[i][1];
+    // weighted sum of the partial outputs (independent loads, unrolled)
+    const int ch = tid;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int s = 0;
+    const int nf = ns < 1024 ? ns : 1024;
+    for (; s + 4 <= nf; s += 4) {
+        a0 += fs[s] * part[(s + 0) * pstride + 2 + ch];
+        a1 += fs[s + 1] * part[(s + 1) * pstride + 2 + ch];
+        a2 += fs[s + 2] * part[(s + 2) * pstride + 2 + ch];
+        a3 += fs[s + 3] * part[(s + 3) * pstride + 2 + ch];
     }
-    if (threadIdx.x < nrows && p.rowstats) {
-        const int r = row0 + threadIdx.x;
-        const int h = kvh * p.g + r / p.M, m = r % p.M;
-        const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
-        p.rowstats[2 * row] = rowM[threadIdx.x];
-        p.rowstats[2 * row + 1] = rowL[threadIdx.x];
+    for (; s < ns; ++s) {
+        float f;
+        if (s < 1024) f = fs[s];
+        else {
+            const float ms = part[s * pstride];
+            f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+        }
+        a0 += f * part[s * pstride + 2 + ch];
+    }
+    const float o = ((a0 + a1) + (a2 + a3)) / L;
+    const int r = row0 + rr;
+    const int h = kvh * p.g + r / p.M, m = r % p.M;
+    const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
+    p.out[row * D + ch] = (_Float16)o;
+    if (ch == 0 && p.rowstats) {
+        p.rowstats[2 * row] = mx;
+        p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
     }
 }
 
 // Normalise the stashed log2-domain logits into attention weights and/or
-// accumulate the importance EMA.  One thread per token.
+// accumulate the importance EMA.  Each thread owns 4 tokens (stride 256).
 __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodeParams p) {
-    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    __shared__ float stats[2 * 512];
     const int64_t rows = (int64_t)p.B * p.Hq * p.M;
-    const int64_t nmax = max(p.N, p.n_scores);
-    if (n >= nmax) return;
-    float imp = 0.f;
-    if (n < p.N) {
-        for (int64_t row = 0; row < rows; ++row) {
-            const float M = p.rowstats[2 * row], L = p.rowstats[2 * row + 1];
-            const float s = p.stash[row * p.N + n];
-            const float e = (M == -INFINITY) ? 0.f : exp2f(s - M);
-            const float w = e / L;
-            if (p.attn_out) p.attn_out[row * p.N + n] = w;
-            imp += w;
+    const int64_t n0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    float imp[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t r0 = 0; r0 < rows; r0 += 512) {
+        const int nr = (int)min((int64_t)512, rows - r0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < 2 * nr; i += 256) stats[i] = p.rowstats[2 * r0 + i];
+        __syncthreads();
+        for (int rr = 0; rr < nr; ++rr) {
+            const float M = stats[2 * rr], L = stats[2 * rr + 1];
+            const float *srow = p.stash + (r0 + rr) * p.N;
+            float *arow = p.attn_out ? p.attn_out + (r0 + rr) * p.N : nullptr;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t n = n0 + 256 * i;
+                if (n < p.N) {
+                    const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(srow[n] - M);
+                    const float w = e / L;
+                    if (arow) arow[n] = w;
+                    imp[i] += w;
+                }
+            }
         }
     }
-    if (p.scores && n < p.n_scores) {
-        // mean over (batch, head), summed over query positions
-        const float mean = imp / (float)(p.B * p.Hq);
-        float sc = p.scores[n] * p.decay;
-        sc = sc + mean;
-        p.scores[n] = sc;
+    if (!p.scores) return;
+    const float bhn = (float)(p.B * p.Hq);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + 256 * i;
+        if (n < p.n_scores) {
+            // mean over (batch, head), summed over query positions
+            float sc = p.scores[n] * p.decay;
+            sc = sc + imp[i] / bhn;
+            p.scores[n] = sc;
+        }
     }
 }
 
@@ -616,10 +833,13 @@ __global__ __launch_bounds__(1024) void legacy_sym_kernel(const void *kz, const 
 template <int D, int KB, int VB, int WK>
 static hipError_t launch_split(const DecodeParams &p, hipStream_t stream) {
     dim3 grid(p.nsplit, p.Hkv, p.B * p.nchunk);
-    const size_t lds_stage = 4 * WaveLds<D>::BYTES;
-    const size_t lds_merge = (size_t)(2 * 4 * 16 + 4 * 16 * D) * 4;
+    const size_t lds_stage = kNW * 2816;
+    const size_t lds_merge = (size_t)(2 * kNW * 16 + kNW * 16 * D) * 4;
     const size_t lds = lds_stage > lds_merge ? lds_stage : lds_merge;
-    hipLaunchKernelGGL((decode_split_kernel<D, KB, VB, WK>), grid, dim3(256), lds, stream, p);
+    if (WK == AKV_WARM_AFFINE && p.n_out > 0)
+        hipLaunchKernelGGL((decode_split_kernel<D, KB, VB, WK, WK == AKV_WARM_AFFINE>), grid, dim3(256), lds, stream, p);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<D, KB, VB, WK, false>), grid, dim3(256), lds, stream, p);
     return hipGetLastError();
 }
 
@@ -652,12 +872,13 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
     }
     e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
-    if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, dim3(p.B * p.Hkv * p.nchunk), dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(decode_reduce_kernel<128>, dim3(p.B * p.Hkv * p.nchunk), dim3(256), 0, s, p);
+    const dim3 rgrid(p.B * p.Hkv * p.nchunk, p.prows);
+    if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, s, p);
+    else hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(128), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (p.stash) {
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
-        hipLaunchKernelGGL(weights_importance_kernel, dim3((unsigned)((nmax + 255) / 256)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(weights_importance_kernel, dim3((unsigned)((nmax + 1023) / 1024)), dim3(256), 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     return hipSuccess;
