@@ -66,7 +66,7 @@ void make_plan(const akv_decode_args *a, Plan *pl) {
     pl->n_wsplit = nw > 0 ? (int)((nw + pl->wsplit_len - 1) / pl->wsplit_len) : 0;
     pl->n_hsplit = nh > 0 ? (int)((nh + pl->hsplit_len - 1) / pl->hsplit_len) : 0;
     pl->nsplit = pl->n_wsplit + pl->n_hsplit;
-    pl->part_bytes = align256(pairs * pl->nsplit * (int64_t)pl->prows * (a->D + 2) * 4);
+    pl->part_bytes = align256(pairs * pl->nsplit * (int64_t)pl->prows * (a->D + 4) * 4);
     pl->rowstat_bytes = align256((int64_t)a->B * a->Hq * a->M * 2 * 4);
     pl->flag_bytes = 256;
     const bool need_stash = a->attn_weights == nullptr && a->scores != nullptr;

@@ -673,7 +673,7 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
             }
         }
     __syncthreads();
-    float *part = p.part + ((bh * p.nchunk + chunk) * p.nsplit + split) * (int64_t)(p.prows * (D + 2));
+    float *part = p.part + ((bh * p.nchunk + chunk) * p.nsplit + split) * (int64_t)(p.prows * (D + 4));
     for (int e = threadIdx.x; e < nrows * D; e += 256) {
         const int rr = e / D, ch = e % D;
         float mx = -INFINITY;
@@ -687,20 +687,24 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
             a += f * alds[(w * 16 + rr) * D + ch];
             l += f * llds[w * 16 + rr];
         }
-        part[rr * (D + 2) + 2 + ch] = a;
+        part[rr * (D + 4) + 4 + ch] = a;
         if (ch == 0) {
-            part[rr * (D + 2) + 0] = mx;
-            part[rr * (D + 2) + 1] = l;
+            part[rr * (D + 4) + 0] = mx;
+            part[rr * (D + 4) + 1] = l;
         }
     }
 }
 
 // Merge the split partials of one query row: out = sum_s f_s acc_s / sum_s f_s l_s,
-// f_s = exp2(m_s - M).  One workgroup (D threads) per (batch, kv-head, chunk, row).
+// f_s = exp2(m_s - M).  One workgroup of 256 threads per (batch, kv-head, chunk,
+// row): thread = (channel quad q, split lane sl); each thread keeps its splits'
+// float4 loads in flight, the split lanes are summed through LDS.
 template <int D>
-__global__ __launch_bounds__(D) void decode_reduce_kernel(const DecodeParams p) {
+__global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p) {
+    constexpr int NQ = D / 4, SL = 256 / NQ, PS = D + 4;
     __shared__ float fs[1024];
-    __shared__ float red[D / 64][2];
+    __shared__ float red[4][2];
+    __shared__ f4 accl[SL][NQ];
     const int bhc = blockIdx.x, rr = blockIdx.y;
     const int chunk = bhc % p.nchunk;
     const int64_t bh = bhc / p.nchunk;
@@ -708,101 +712,102 @@ __global__ __launch_bounds__(D) void decode_reduce_kernel(const DecodeParams p) 
     const int row0 = chunk * 16, nrows = min(16, p.R - row0);
     if (rr >= nrows) return;
     const int ns = p.nsplit;
-    const int64_t pstride = (int64_t)p.prows * (D + 2);
-    const float *part = p.part + (bh * p.nchunk + chunk) * (int64_t)ns * pstride + rr * (D + 2);
+    const int64_t pstride = (int64_t)p.prows * PS;
+    const float *part = p.part + (bh * p.nchunk + chunk) * (int64_t)ns * pstride + rr * PS;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    // row max over the splits
     float mx = -INFINITY;
-    for (int s = tid; s < ns; s += D) mx = fmaxf(mx, part[s * pstride]);
+    for (int s = tid; s < ns; s += 256) mx = fmaxf(mx, part[s * pstride]);
     for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if (lane == 0) red[w][0] = mx;
     __syncthreads();
-    mx = red[0][0];
-#pragma unroll
-    for (int i = 1; i < D / 64; ++i) mx = fmaxf(mx, red[i][0]);
-    // split factors and the row sum
+    mx = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
     float l = 0.f;
-    for (int s = tid; s < ns; s += D) {
+    for (int s = tid; s < ns; s += 256) {
         const float ms = part[s * pstride];
         const float f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
         if (s < 1024) fs[s] = f;
         l += f * part[s * pstride + 1];
     }
     for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    __syncthreads();
     if (lane == 0) red[w][1] = l;
     __syncthreads();
-    float L = 0.f;
+    const float L = (red[0][1] + red[1][1]) + (red[2][1] + red[3][1]);
+    const int q = tid % NQ, sl = tid / NQ;
+    f4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
+    int s = sl;
+    for (; s + SL < ns; s += 2 * SL) {
+        const f4 x0 = *(const f4 *)(part + s * pstride + 4 + 4 * q);
+        const f4 x1 = *(const f4 *)(part + (s + SL) * pstride + 4 + 4 * q);
+        const float f0 = s < 1024 ? fs[s] : 0.f, f1 = s + SL < 1024 ? fs[s + SL] : 0.f;
+        a0 += f0 * x0;
+        a1 += f1 * x1;
+    }
+    for (; s < ns; s += SL) {
+        const f4 x0 = *(const f4 *)(part + s * pstride + 4 + 4 * q);
+        a0 += (s < 1024 ? fs[s] : 0.f) * x0;
+    }
+    for (s = 1024 + sl; s < ns; s += SL) {  // more than 1024 splits: factors not cached
+        const float ms = part[s * pstride];
+        const float f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+        a0 += f * *(const f4 *)(part + s * pstride + 4 + 4 * q);
+    }
+    accl[sl][q] = a0 + a1;
+    __syncthreads();
+    if (tid < D) {
+        const int qq = tid / 4, e = tid % 4;
+        float o = 0.f;
 #pragma unroll
-    for (int i = 0; i < D / 64; ++i) L += red[i][1];
-    // weighted sum of the partial outputs (independent loads, unrolled)
-    const int ch = tid;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    int s = 0;
-    const int nf = ns < 1024 ? ns : 1024;
-    for (; s + 4 <= nf; s += 4) {
-        a0 += fs[s] * part[(s + 0) * pstride + 2 + ch];
-        a1 += fs[s + 1] * part[(s + 1) * pstride + 2 + ch];
-        a2 += fs[s + 2] * part[(s + 2) * pstride + 2 + ch];
-        a3 += fs[s + 3] * part[(s + 3) * pstride + 2 + ch];
-    }
-    for (; s < ns; ++s) {
-        float f;
-        if (s < 1024) f = fs[s];
-        else {
-            const float ms = part[s * pstride];
-            f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+        for (int k = 0; k < SL; ++k) o += accl[k][qq][e];
+        o = o / L;
+        const int r = row0 + rr;
+        const int h = kvh * p.g + r / p.M, m = r % p.M;
+        const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
+        p.out[row * D + tid] = (_Float16)o;
+        if (tid == 0 && p.rowstats) {
+            p.rowstats[2 * row] = mx;
+            p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
         }
-        a0 += f * part[s * pstride + 2 + ch];
-    }
-    const float o = ((a0 + a1) + (a2 + a3)) / L;
-    const int r = row0 + rr;
-    const int h = kvh * p.g + r / p.M, m = r % p.M;
-    const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
-    p.out[row * D + ch] = (_Float16)o;
-    if (ch == 0 && p.rowstats) {
-        p.rowstats[2 * row] = mx;
-        p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
     }
 }
 
 // Normalise the stashed log2-domain logits into attention weights and/or
-// accumulate the importance EMA.  Each thread owns 4 tokens (stride 256).
+// accumulate the importance EMA.  Workgroup = 64 tokens x 16 row lanes: thread
+// (token t, row lane rl) walks rows rl, rl+16, ... for tokens t, t+16, t+32,
+// t+48; the row lanes are summed through LDS.
 __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodeParams p) {
-    __shared__ float stats[2 * 512];
+    __shared__ float red[16][65];
     const int64_t rows = (int64_t)p.B * p.Hq * p.M;
-    const int64_t n0 = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+    const int t = threadIdx.x & 15, rl = threadIdx.x >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * 64 + t;
     float imp[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t r0 = 0; r0 < rows; r0 += 512) {
-        const int nr = (int)min((int64_t)512, rows - r0);
-        __syncthreads();
-        for (int i = threadIdx.x; i < 2 * nr; i += 256) stats[i] = p.rowstats[2 * r0 + i];
-        __syncthreads();
-        for (int rr = 0; rr < nr; ++rr) {
-            const float M = stats[2 * rr], L = stats[2 * rr + 1];
-            const float *srow = p.stash + (r0 + rr) * p.N;
-            float *arow = p.attn_out ? p.attn_out + (r0 + rr) * p.N : nullptr;
+    const int64_t N = p.N;
+    for (int64_t r = rl; r < rows; r += 16) {
+        const float M = p.rowstats[2 * r], inv = 1.0f / p.rowstats[2 * r + 1];
+        float *srow = p.stash + r * N;
+        float x[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int64_t n = n0 + 256 * i;
-                if (n < p.N) {
-                    const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(srow[n] - M);
-                    const float w = e / L;
-                    if (arow) arow[n] = w;
-                    imp[i] += w;
-                }
-            }
+        for (int i = 0; i < 4; ++i) x[i] = (n0 + 16 * i < N) ? srow[n0 + 16 * i] : -INFINITY;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[i] - M);
+            const float wgt = e * inv;
+            if (p.attn_out && n0 + 16 * i < N) srow[n0 + 16 * i] = wgt;
+            imp[i] += (n0 + 16 * i < N) ? wgt : 0.f;
         }
     }
     if (!p.scores) return;
-    const float bhn = (float)(p.B * p.Hq);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int64_t n = n0 + 256 * i;
+    for (int i = 0; i < 4; ++i) red[rl][16 * i + t] = imp[i];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) s += red[k][threadIdx.x];
+        const int64_t n = (int64_t)blockIdx.x * 64 + threadIdx.x;
         if (n < p.n_scores) {
             // mean over (batch, head), summed over query positions
             float sc = p.scores[n] * p.decay;
-            sc = sc + imp[i] / bhn;
+            sc = sc + s / (float)(p.B * p.Hq);
             p.scores[n] = sc;
         }
     }
@@ -873,12 +878,12 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
     e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
     const dim3 rgrid(p.B * p.Hkv * p.nchunk, p.prows);
-    if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(64), 0, s, p);
-    else hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(128), 0, s, p);
+    if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(256), 0, s, p);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     if (p.stash) {
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
-        hipLaunchKernelGGL(weights_importance_kernel, dim3((unsigned)((nmax + 1023) / 1024)), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(weights_importance_kernel, dim3((unsigned)((nmax + 63) / 64)), dim3(256), 0, s, p);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     return hipSuccess;
