@@ -43,29 +43,78 @@ struct Plan {
 
 constexpr int kWaves = 4;
 
-// Deterministic split schedule: about `target` splits per (batch, kv-head,
-// row chunk), each a multiple of the K meta unit (warm) or 16 tokens (hot),
-// and at least one unit per wave.
+// Deterministic split schedule.  Splits are sized by bytes so a hot split (fp16
+// K/V, 4*D bytes per token) and a warm split (packed codes + meta) stream
+// about the same amount; each is a multiple of its token unit and holds at
+// least one unit per wave.  Without an explicit count the schedule aims at a
+// few workgroups per compute unit of the 256-CU MI355X.
+constexpr int kCUs = 256;
+
+bool fast_path(const akv_decode_args *a) {
+    const akv_warm_desc &w = a->warm;
+    return w.kind == AKV_WARM_AFFINE && a->D == 128 && w.block_t % 32 == 0 && w.n_out == 0 &&
+           (w.group_v == 32 || w.group_v == 64 || w.group_v == 128);
+}
+
 void make_plan(const akv_decode_args *a, Plan *pl) {
     const akv_warm_desc &w = a->warm;
     const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
     const int64_t nh = a->n_hot;
     const int g = a->Hq / a->Hkv;
     const int R = g * a->M;
+    const bool fast = fast_path(a);
     pl->nchunk = (R + 15) / 16;
     pl->prows = R < 16 ? R : 16;
     pl->N = nw + nh;
     const int64_t pairs = (int64_t)a->B * a->Hkv * pl->nchunk;
-    int64_t target = a->num_splits > 0 ? a->num_splits : (1024 + pairs - 1) / pairs;
+    // bytes streamed per token
+    double bw = 0.0;
+    if (w.kind == AKV_WARM_AFFINE)
+        bw = a->D * (w.bits_k + w.bits_v) / 8.0 + 4.0 * a->D / w.block_t + 4.0 * a->D / w.group_v;
+    else if (w.kind == AKV_WARM_LEGACY)
+        bw = 2.0 * a->D * w.bits_k / 8.0 + 4.0 * a->D / (w.group_size > 0 ? w.group_size : 32);
+    const double bhot = 4.0 * a->D;
+    if (fast) {
+        // One workgroup of many waves per CU and (batch, kv-head, row chunk);
+        // its waves share the range's hot tiles and warm units dynamically.
+        const int64_t units = (nw + 31) / 32, tiles = (nh + 15) / 16;
+        int64_t cp = a->num_splits > 0 ? a->num_splits : kCUs / pairs;
+        const int64_t by_items = (units + tiles) / (2 * akv::decode_fast_waves());
+        if (a->num_splits <= 0 && cp > by_items) cp = by_items;
+        if (cp < 1) cp = 1;
+        pl->wsplit_len = (units + cp - 1) / cp * 32;
+        pl->hsplit_len = (tiles + cp - 1) / cp * 16;
+        if (pl->wsplit_len < 32) pl->wsplit_len = 32;
+        if (pl->hsplit_len < 16) pl->hsplit_len = 16;
+        pl->n_wsplit = (int)cp;
+        pl->n_hsplit = 0;
+        pl->nsplit = (int)cp;
+    } else {
+    int64_t target;
+    if (a->num_splits > 0) {
+        target = a->num_splits;
+    } else {
+        target = (kCUs * 4 + pairs - 1) / pairs;
+    }
     if (target < 1) target = 1;
-    const int64_t unit = (w.kind == AKV_WARM_AFFINE) ? w.block_t : 16;
-    int64_t len = (pl->N + target - 1) / target;
-    if (len < 1) len = 1;
-    pl->wsplit_len = round_up(len > kWaves * unit ? len : kWaves * unit, unit);
-    pl->hsplit_len = round_up(len > kWaves * 16 ? len : kWaves * 16, 16);
+    // Hot splits first (each about one split's worth of bytes), then the warm
+    // tier takes the rest of the target, so the grid never exceeds it: a grid
+    // one workgroup over the resident capacity runs a second, nearly idle round.
+    const double pair_bytes = nw * bw + nh * bhot;
+    const double split_bytes = pair_bytes / (double)target;
+    const int64_t wunit = (w.kind == AKV_WARM_AFFINE) ? w.block_t : 16;
+    int64_t n_h = nh > 0 ? (int64_t)std::ceil(nh * bhot / split_bytes - 1e-9) : 0;
+    if (nh > 0 && n_h < 1) n_h = 1;
+    if (nw > 0 && n_h > target - 1) n_h = target > 1 ? target - 1 : 1;
+    const int64_t n_w = nw > 0 ? (target - n_h > 1 ? target - n_h : 1) : 0;
+    const int64_t hlen = n_h > 0 ? (nh + n_h - 1) / n_h : 0;
+    const int64_t wlen = n_w > 0 ? (nw + n_w - 1) / n_w : 0;
+    pl->wsplit_len = round_up(wlen > kWaves * wunit ? wlen : kWaves * wunit, wunit);
+    pl->hsplit_len = round_up(hlen > kWaves * 16 ? hlen : kWaves * 16, 16);
     pl->n_wsplit = nw > 0 ? (int)((nw + pl->wsplit_len - 1) / pl->wsplit_len) : 0;
     pl->n_hsplit = nh > 0 ? (int)((nh + pl->hsplit_len - 1) / pl->hsplit_len) : 0;
     pl->nsplit = pl->n_wsplit + pl->n_hsplit;
+    }
     pl->part_bytes = align256(pairs * pl->nsplit * (int64_t)pl->prows * (a->D + 4) * 4);
     pl->rowstat_bytes = align256((int64_t)a->B * a->Hq * a->M * 2 * 4);
     pl->flag_bytes = 256;
@@ -221,6 +270,7 @@ int akv_decode_attn(const akv_decode_args *a, void *stream) {
     p.scores = a->scores;
     p.n_scores = a->scores ? a->n_scores : 0;
     p.decay = a->decay;
+    if (w.kind == AKV_WARM_AFFINE) p.slot_bytes = (int)akv::decode_fast_slot_bytes(kb, vb, w.group_v);
     hipError_t e = akv::decode_launch(p, kb, vb, wk, sym_ptr, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     return ok();

@@ -44,6 +44,8 @@ struct DecodeParams {
     float *scores;                // importance EMA (or null)
     int64_t n_scores;
     float decay;
+    // fast path (decode_fast.hip): bytes of one LDS ring slot
+    int slot_bytes;
 };
 
 // Launch split + reduce (+ weights/importance) kernels.  `sym_src` = {meta dtype, count}
@@ -52,5 +54,12 @@ struct DecodeParams {
 hipError_t legacy_sym_launch(const void *kz, const void *vz, int64_t n, int dt, int *flags, hipStream_t s);
 
 hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const int *sym_src, hipStream_t s);
+
+// LDS-streamed split kernel for the block-affine tier (decode_fast.hip).
+bool decode_fast_eligible(const DecodeParams &p, int wk);
+int64_t decode_fast_slot_bytes(int kb, int vb, int Gv);
+int64_t decode_fast_lds_bytes(int64_t slot_bytes);
+int decode_fast_waves();
+hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, hipStream_t s);
 
 }  // namespace akv

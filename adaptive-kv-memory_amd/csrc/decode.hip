@@ -875,7 +875,8 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
         e = legacy_sym_launch(p.kz, p.vz, (int64_t)sym_src_dt_n[1], sym_src_dt_n[0], (int *)p.sym_flags, s);
         if (e != hipSuccess) return e;
     }
-    e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
+    if (decode_fast_eligible(p, wk)) e = decode_fast_split_launch(p, kb, vb, s);
+    else e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
     const dim3 rgrid(p.B * p.Hkv * p.nchunk, p.prows);
     if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(256), 0, s, p);

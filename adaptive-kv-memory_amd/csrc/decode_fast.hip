@@ -1,0 +1,776 @@
+// Split-K fused dequant-attention over the block-affine warm tier, streamed
+// through LDS: the decode kernel of the 32k-context workload.
+//
+// Scope: head_dim 128, K blocks of T tokens with T a multiple of 32, V groups
+// of G = 32, 64 or 128 channels, no outlier channels, 2/3/4 bits for K and V.
+// Other shapes use decode_split_kernel (decode.hip).
+//
+// Work split: grid (split, kv-head, batch * row-chunk); a workgroup of 4
+// waves owns one (batch, kv-head) and one contiguous token range of either
+// the warm or the hot segment.  Each wave walks its own units (warm: 32-token
+// blocks; hot: the K or the V half of a 16-token tile) round-robin over the
+// range, through a private ring of NS LDS slots filled by buffer loads that
+// write LDS directly (16 B per lane).  A unit's six arrays (K codes, V codes,
+// K scale, K zero, V scale, V zero) are each one contiguous byte range, so a
+// slot fills with 6-8 wave-wide loads whose offsets are scalars; ranges past
+// the end of a (batch, kv-head) read as zero (buffer range check), which
+// keeps ragged tails in bounds.  The loads of units i+1 .. i+NS-1 stay in
+// flight while unit i is computed.
+//
+// Per 16-token tile a wave does:
+//   QK:  S^T[16 tok x 16 rows] = K . Q^T, 4 x v_mfma_f32_16x16x32_f16.  Lane
+//        (token l%16, channel group l/16) builds its 32 K values from 3-4
+//        byte-permuted windows of its packed row: one and-or puts a code pair
+//        into the mantissas of two fp16 numbers 2^(10-o) + c (o = the code's
+//        bit offset in the window), one packed fma with (s, -2^(10-o) s)
+//        gives round16(c*s) exactly, one packed add gives round16(. + z): the
+//        reference's fp16 dequant bit for bit.  The per-channel (s, n, z)
+//        pairs of a block are prepared once per wave in LDS.
+//   softmax: online, log2 domain, lazy rescale (threshold 2^8); probabilities
+//        enter PV as fp16 scaled by 2^7.
+//   PV:  O^T[16 chunks x 16 rows] += V^T . P^T, 8 x v_mfma_f32_16x16x16_f16.
+//        Lane (chunk l%16 of 8 channels, tokens 4(l/16)..+3) pairs two tokens
+//        per dword with byte permutes and shifts, then the same exact
+//        and-or / fma / add dequant with the token's (s, z) of its group.
+// The 4 waves merge in LDS and write one (m, l, acc) partial per workgroup;
+// decode_reduce_kernel merges the splits.
+//
+// A block whose scales would overflow -2^(10-o) s in fp16 (|s| >= 64) takes
+// a slower exact path: the code is recovered as an fp16 integer, then
+// round16(c * s) and round16(. + z) are two packed ops.
+#include "akv_common.h"
+#include "decode.h"
+
+namespace akv {
+
+namespace {
+
+constexpr int kD = 128;
+constexpr int kWaves = 12;           // waves per workgroup (one workgroup per CU, 3 per SIMD)
+constexpr int kUnit = 32;            // warm tokens per ring slot
+constexpr int kNS = 2;               // ring slots per wave
+constexpr int kKmetaBytes = 3 * 4 * 16 * 4;  // [s | n | z][group][pair] u32
+constexpr int kHotLoads = 4;         // 16 tokens x 256 B = 4 KiB = 4 wave loads
+constexpr float kThreshF = 8.0f;
+constexpr float kPLog2F = 7.0f;
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+// Buffer resource as four scalars (raw buffer, no stride, range-checked to `bytes`).
+__device__ __forceinline__ u4 rsrc4(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)base;
+    return (u4){(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, bytes, (uint32_t)kRsrcWord3};
+}
+
+// One LDS-DMA instruction: for each lane i set in `mask`, 16 bytes at buffer
+// offset soff + voff_i are written to LDS [lds + 16 i]; bytes past the
+// resource range arrive as zeros.  Written as one asm block so the compiler
+// can neither merge two of them under divergent control flow nor change how
+// many are issued (the vmcnt waits count them); M0 is restored afterwards.
+__device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff, uint64_t mask) {
+    uint64_t saved;
+    uint32_t saved_m0;
+    asm volatile(
+        "s_mov_b32 %[sm0], m0\n\t"
+        "s_mov_b32 m0, %[lds]\n\t"
+        "s_mov_b64 %[sv], exec\n\t"
+        "s_and_b64 exec, exec, %[mask]\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %[voff], %[rsrc], %[soff] offen lds\n\t"
+        "s_mov_b64 exec, %[sv]\n\t"
+        "s_mov_b32 m0, %[sm0]"
+        : [sv] "=&s"(saved), [sm0] "=&s"(saved_m0)
+        : [lds] "s"(lds), [mask] "s"(mask), [voff] "v"(voff), [rsrc] "s"(rsrc), [soff] "s"(soff)
+        : "memory");
+}
+__device__ __forceinline__ uint64_t lane_mask(int bytes) {  // lanes covering `bytes` (>= 16)
+    return bytes >= 1024 ? ~0ull : ((1ull << (bytes >> 4)) - 1ull);
+}
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char *p) { return (uint32_t)(uintptr_t)p; }
+
+// A value the compiler must keep in a VGPR (not rematerialize as a literal),
+// so (x & m) | c selects one v_and_or_b32 with m in a VGPR and c in an SGPR.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ h2 pk_fma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
+
+__device__ __forceinline__ float wmax16(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+__device__ __forceinline__ float wsum16(float x) {
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+// fp16 bits of 2^(10-o): a code at bit offset o of that number's mantissa reads as 2^(10-o) + c.
+__host__ __device__ constexpr uint32_t magic_of(int o) { return (uint32_t)(25 - o) << 10; }
+__host__ __device__ constexpr uint32_t magic2(int o) { return magic_of(o) * 0x00010001u; }
+__host__ __device__ constexpr float magic_val(int o) { return (float)(1 << (10 - o)); }
+
+// --------------------------------------------------------------- K windows
+// Pair pi (0..15) of a lane's 32 channels: window dword and bit offset; the
+// channels (relative to the lane's group) of its halves are kpair_chan().
+template <int BK>
+__host__ __device__ constexpr int koff(int pi) {
+    return BK == 3 ? ((pi % 8) == 0 ? 0 : (pi % 8) == 1 ? 3 : (pi % 8) == 2 ? 6 : (pi % 8) == 3 ? 1
+                      : (pi % 8) == 4 ? 4 : (pi % 8) == 5 ? 7 : (pi % 8) == 6 ? 2 : 5)
+         : BK == 4 ? (pi % 2) * 4
+                   : 2 * (pi % 4);
+}
+template <int BK>
+struct KWin {
+    uint32_t w[BK == 3 ? 6 : (BK == 4 ? 8 : 4)];
+};
+// r: the lane's raw code bytes (BK*4 bytes) as little-endian dwords
+template <int BK>
+__device__ __forceinline__ void k_windows(const uint32_t *r, KWin<BK> &W) {
+    if (BK == 3) {
+        W.w[0] = perm(r[1], r[0], 0x04050102u);
+        W.w[1] = perm(r[1], r[0], 0x03040001u);
+        W.w[2] = perm(r[1], r[0], 0x0C030C00u);
+        W.w[3] = perm(r[2], r[1], 0x06070304u);
+        W.w[4] = perm(r[2], r[1], 0x05060203u);
+        W.w[5] = perm(r[2], r[1], 0x0C050C02u);
+    } else if (BK == 4) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            W.w[2 * d] = r[d];
+            W.w[2 * d + 1] = perm(0u, r[d], 0x0C030C01u);
+        }
+    } else {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            W.w[2 * d] = r[d];
+            W.w[2 * d + 1] = perm(0u, r[d], 0x0C030C01u);
+        }
+    }
+}
+template <int BK>
+__device__ __forceinline__ uint32_t k_window_of(const KWin<BK> &W, int pi) {
+    if (BK == 3) {
+        const int k = pi % 8, base = 3 * (pi / 8);
+        return W.w[base + (k < 3 ? 0 : (k < 6 ? 1 : 2))];
+    } else if (BK == 4) {
+        return W.w[2 * (pi / 4) + ((pi % 4) >= 2 ? 1 : 0)];
+    } else {
+        return W.w[2 * (pi / 8) + ((pi % 8) >= 4 ? 1 : 0)];
+    }
+}
+
+// --------------------------------------------------------------- V windows
+// One token pair (a, b) of an 8-channel chunk.  da / db: the chunk's bytes
+// of each token at byte 0 of a dword (memory order).  Code k (channel k of
+// the chunk) sits in window vwin(k) at bit offset voff(k), in both halves.
+template <int BV>
+struct VSlot {
+    static constexpr int NW = BV == 3 ? 3 : (BV == 4 ? 4 : 2);
+};
+template <int BV>
+__host__ __device__ constexpr int vwin(int k) {
+    // 3-bit: codes 7,6,5 in window 0; 4,3,2 in 1; 1,0 in 2
+    // 4-bit: ch1,ch0 in 0; ch3,ch2 in 1; ch5,ch4 in 2; ch7,ch6 in 3
+    // 2-bit: codes 3..0 in 0; 7..4 in 1
+    return BV == 3 ? (k >= 5 ? 0 : (k >= 2 ? 1 : 2)) : BV == 4 ? (k / 2) : (k / 4);
+}
+template <int BV>
+__host__ __device__ constexpr int voff(int k) {
+    return BV == 3 ? (k >= 5 ? 3 * (7 - k) : (k >= 2 ? 3 * (4 - k) : 3 * (1 - k)))
+         : BV == 4 ? ((k & 1) ? 0 : 4)
+                   : 2 * (3 - (k & 3));
+}
+template <int BV>
+__device__ __forceinline__ void v_windows(uint32_t da, uint32_t db, uint32_t *win) {
+    if (BV == 3) {
+        win[0] = perm(db, da, 0x05060102u);            // [a.x2 a.x1 | b.x2 b.x1]: W bits 0-15
+        const uint32_t w1 = perm(db, da, 0x04050001u); // [a.x1 a.x0 | b.x1 b.x0]: W bits 8-23
+        win[1] = w1 >> 1;
+        win[2] = w1 >> 10;
+    } else if (BV == 4) {
+        const uint32_t lo = perm(db, da, 0x05040100u); // bytes 0,1 of a | of b
+        const uint32_t hi = perm(db, da, 0x07060302u); // bytes 2,3
+        win[0] = lo;
+        win[1] = lo >> 8;
+        win[2] = hi;
+        win[3] = hi >> 8;
+    } else {
+        const uint32_t w = perm(db, da, 0x05040100u);  // bytes 0,1 of a | of b
+        win[0] = w;
+        win[1] = w >> 8;
+    }
+}
+template <int BV>
+__host__ __device__ constexpr int v_ostep() { return BV == 3 ? 3 : (BV == 4 ? 4 : 2); }
+template <int BV>
+__host__ __device__ constexpr int v_noffs() { return BV == 3 ? 3 : (BV == 4 ? 2 : 4); }
+
+// Masks of a code at bit offset o (both halves), one VGPR per offset 0..7.
+template <int B>
+struct Masks {
+    uint32_t m[8];
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int o = 0; o < 8; ++o) m[o] = in_vgpr((((1u << B) - 1u) << o) * 0x00010001u);
+    }
+};
+
+// --------------------------------------------------------------- layouts
+template <int BK, int BV, int NG>
+struct WarmLayout {
+    static constexpr int KR = 16 * BK, VR = 16 * BV;  // packed row bytes (D = 128)
+    static constexpr int KCB = kUnit * KR, VCB = kUnit * VR;
+    static constexpr int VMB = 64 * NG;               // V scale (or zero) bytes of 32 tokens
+    static constexpr int NKC = (KCB + 1023) / 1024, NVC = (VCB + 1023) / 1024;
+    static constexpr int NLOAD = NKC + NVC + 4;
+    static constexpr int KC = 0, VC = KCB, KS = KCB + VCB, KZ = KS + 256, VS = KZ + 256, VZ = VS + VMB;
+    static constexpr int BYTES = VZ + VMB;
+};
+
+struct WarmRes {
+    u4 kc, vc, ks, kz, vs, vz;
+};
+
+template <int BK, int BV, int NG>
+__device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T) {
+    using L = WarmLayout<BK, BV, NG>;
+    const uint32_t v16 = (uint32_t)lane * 16u;
+    const uint32_t base = lds_addr(slot);
+#pragma unroll
+    for (int i = 0; i < L::NKC; ++i)
+        dma16(R.kc, base + L::KC + 1024 * i, v16, (uint32_t)u * L::KCB + 1024u * i, lane_mask(L::KCB - 1024 * i));
+#pragma unroll
+    for (int i = 0; i < L::NVC; ++i)
+        dma16(R.vc, base + L::VC + 1024 * i, v16, (uint32_t)u * L::VCB + 1024u * i, lane_mask(L::VCB - 1024 * i));
+    const uint32_t kmrow = (uint32_t)((u * kUnit) / T) * 256u;
+    dma16(R.ks, base + L::KS, v16, kmrow, 0xFFFFull);
+    dma16(R.kz, base + L::KZ, v16, kmrow, 0xFFFFull);
+    dma16(R.vs, base + L::VS, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+    dma16(R.vz, base + L::VZ, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+}
+
+__device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, int tile) {
+    const uint32_t base = lds_addr(slot);
+#pragma unroll
+    for (int i = 0; i < kHotLoads; ++i)
+        dma16(r, base + 1024 * i, (uint32_t)lane * 16u, (uint32_t)tile * 4096u + 1024u * i, ~0ull);
+}
+
+struct Soft {
+    float m2, l;
+    f4 acc[8];
+};
+
+// Online softmax over one 16-token tile.  s: raw q.k of tokens 4*grp+i for
+// row col.  The running max of a row only moves when some score exceeds it by
+// more than 2^8 (log2 units); the test needs no cross-lane traffic, since a
+// row's tile max passes the bound iff one of its four lanes' maxima does.  On
+// the rare update the four lanes of a row agree on the new max through two
+// shuffles.  Returns the fp16 P^T operand (x 2^7).
+__device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
+    const float t = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])) * sl2;
+    if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
+        const float tm2 = wmax16(t);
+        const float mn = fmaxf(st.m2, tm2);
+        const float alpha = __builtin_amdgcn_exp2f(st.m2 - mn);
+        st.l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
+        st.m2 = mn;
+    }
+    const float bias = kPLog2F - st.m2;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, bias));
+    st.l += (p[0] + p[1]) + (p[2] + p[3]);
+    return (h4){(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+}
+
+__device__ __forceinline__ void stash4(const DecodeParams &p, int64_t strow, int row_valid, int64_t n0, f4 s,
+                                       float sl2, int nvalid) {
+    if (!p.stash || !row_valid) return;
+    float *dst = p.stash + strow + n0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (i < nvalid) dst[i] = s[i] * sl2;
+}
+
+__device__ __forceinline__ uint32_t lds_u16(const unsigned char *p) { return *(const uint16_t *)p; }
+__device__ __forceinline__ h2 lds_h2(const unsigned char *a, const unsigned char *b) {
+    return (h2){*(const _Float16 *)a, *(const _Float16 *)b};
+}
+__device__ __forceinline__ bool finite2(uint32_t x) {
+    return ((x & 0x7C00u) != 0x7C00u) && ((x & 0x7C000000u) != 0x7C000000u);
+}
+
+}  // namespace
+
+
+// Work item kinds of a ring slot.
+constexpr int kNone = 0, kWarm = 1, kHotK = 2, kHotV = 3;
+
+// Natural-order hot K (16 dwords of channel pairs 2d, 2d+1 of the lane's 32
+// channels) -> the warm pair order: pair pi holds channels kpair_chan(pi, 0/1),
+// which always have the same parity, so one byte permute builds each pair.
+template <int BK>
+__device__ __forceinline__ void hot_k_pairs(const uint32_t *nat, uint32_t *pairs) {
+#pragma unroll
+    for (int pi = 0; pi < 16; ++pi) {
+        const int c0 = kpair_chan<BK>(pi, 0), c1 = kpair_chan<BK>(pi, 1);
+        const uint32_t sel = (c0 & 1) ? 0x07060302u : 0x05040100u;
+        pairs[pi] = perm(nat[c1 >> 1], nat[c0 >> 1], sel);
+    }
+}
+
+#ifndef AKV_FAST_WAVES_PER_EU
+#define AKV_FAST_WAVES_PER_EU 3
+#endif
+template <int BK, int BV, int NG>
+__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(AKV_FAST_WAVES_PER_EU, AKV_FAST_WAVES_PER_EU)))
+void decode_fast_kernel(const DecodeParams p) {
+    using L = WarmLayout<BK, BV, NG>;
+    constexpr int KSTEPS = kD / 32;
+    constexpr int NLW = L::NLOAD;     // loads of a warm unit
+    constexpr int NLH = kHotLoads;    // loads of a hot half
+    constexpr int GV = kD / NG;       // V group size
+
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+    const int split = blockIdx.x, kvh = blockIdx.y;
+    const int b = blockIdx.z / p.nchunk, chunk = blockIdx.z % p.nchunk;
+    const int row0 = chunk * 16;
+    const int nrows = min(16, p.R - row0);
+    const int slot_bytes = p.slot_bytes;
+    unsigned char *ring = smem + wave * (kNS * slot_bytes + kKmetaBytes);
+    unsigned char *kmeta = ring + kNS * slot_bytes;
+    unsigned *work = (unsigned *)(smem + kWaves * (kNS * slot_bytes + kKmetaBytes));
+
+    const int r = row0 + col;
+    const int row_valid = col < nrows;
+    const int rc = row_valid ? r : row0;
+    const int hq = kvh * p.g + rc / p.M, mq = rc % p.M;
+    const int64_t strow = ((int64_t)(b * p.Hq + hq) * p.M + mq) * p.N;
+    const int64_t bh = (int64_t)b * p.Hkv + kvh;
+    const float sl2 = p.scale_log2;
+    const int64_t warm_base = p.hot_first ? p.n_hot : 0;  // logical position of warm token 0
+    const int64_t hot_base = p.hot_first ? 0 : p.n_warm;
+
+    // this workgroup's items: hot 16-token tiles, then warm 32-token units
+    const int nw = (int)p.n_warm, nh = (int)p.n_hot;
+    const int w_begin = min(split * (int)p.wsplit_len, nw), w_end = min(w_begin + (int)p.wsplit_len, nw);
+    const int h_begin = min(split * (int)p.hsplit_len, nh), h_end = min(h_begin + (int)p.hsplit_len, nh);
+    const int u_first = w_begin / kUnit, n_wu = (w_end + kUnit - 1) / kUnit - u_first;
+    const int t_first = h_begin / 16, n_ht = (h_end + 15) / 16 - t_first;
+    const int n_items = (h_end > h_begin ? n_ht : 0) + (w_end > w_begin ? n_wu : 0);
+    const int n_hot_items = h_end > h_begin ? n_ht : 0;
+    if (threadIdx.x == 0) *work = 0u;
+
+    // Q operand (B of QK): lane = (row col, channel group grp), in the channel
+    // order the warm code pairs come out in (hot K is permuted to match)
+    h8 qop[KSTEPS];
+    {
+        const _Float16 *qrow = p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp;
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) qop[st][j] = qrow[kpair_chan<BK>(4 * st + j / 2, j % 2)];
+    }
+
+    Soft stt;
+    stt.m2 = -INFINITY;
+    stt.l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) stt.acc[j] = (f4){0.f, 0.f, 0.f, 0.f};
+
+    WarmRes R;
+    {
+        const uint32_t nwu = (uint32_t)p.n_warm;
+        R.kc = rsrc4((const unsigned char *)p.kc + bh * p.n_warm * L::KR, nwu * L::KR);
+        R.vc = rsrc4((const unsigned char *)p.vc + bh * p.n_warm * L::VR, nwu * L::VR);
+        R.ks = rsrc4((const _Float16 *)p.ks + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
+        R.kz = rsrc4((const _Float16 *)p.kz + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
+        R.vs = rsrc4((const _Float16 *)p.vs + bh * p.n_warm * NG, nwu * NG * 2);
+        R.vz = rsrc4((const _Float16 *)p.vz + bh * p.n_warm * NG, nwu * NG * 2);
+    }
+    const u4 rkh = rsrc4(p.khot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
+    const u4 rvh = rsrc4(p.vhot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
+
+    Masks<BK> km;
+    km.init();
+    Masks<BV> vmk;
+    if (BV == BK) vmk = *(const Masks<BV> *)&km;
+    else vmk.init();
+    // K meta prep role of this lane: (group g2, pair pi2)
+    const int g2 = lane >> 4, pi2 = lane & 15;
+    const int kch_lo = 32 * g2 + kpair_chan<BK>(pi2, 0), kch_hi = 32 * g2 + kpair_chan<BK>(pi2, 1);
+    const _Float16 nmul = (_Float16)(-magic_val(koff<BK>(pi2)));
+    // V role: chunk col and its group; lane parts of the slot offsets
+    const int gv = (8 * col) / GV;
+    const int k_lane = L::KC + col * L::KR + grp * 4 * BK;
+    const int v_lane = L::VC + 4 * grp * L::VR + (BV == 3 ? 3 * col : BV == 4 ? 4 * col : 2 * col);
+    const int vm_lane = (4 * grp * NG + gv) * 2;
+
+    __syncthreads();  // work counter initialised
+
+    // ---- the ring: slot s holds unit (kind[s], id[s]); a hot item is two units (K, then V)
+    int kind[kNS], uid[kNS];
+    int pend = -1;  // hot tile whose V half is still to be issued
+    auto next_unit = [&](int &k, int &id) {
+        if (pend >= 0) {
+            k = kHotV;
+            id = pend;
+            pend = -1;
+            return;
+        }
+        unsigned it = 0;
+        if (lane == 0) it = atomicAdd(work, 1u);
+        it = __builtin_amdgcn_readfirstlane(it);
+        if ((int)it >= n_items) {
+            k = kNone;
+            id = 0;
+        } else if ((int)it < n_hot_items) {
+            k = kHotK;
+            id = t_first + (int)it;
+            pend = id;
+        } else {
+            k = kWarm;
+            id = u_first + (int)it - n_hot_items;
+        }
+    };
+    auto issue = [&](int k, int id, unsigned char *slot) {
+        if (k == kWarm) issue_warm<BK, BV, NG>(R, slot, lane, id, p.T);
+        else if (k == kHotK) issue_hot(rkh, slot, lane, id);
+        else if (k == kHotV) issue_hot(rvh, slot, lane, id);
+    };
+#pragma unroll
+    for (int s2 = 0; s2 < kNS; ++s2) {
+        next_unit(kind[s2], uid[s2]);
+        issue(kind[s2], uid[s2], ring + s2 * slot_bytes);
+    }
+
+    h4 hot_p = {};  // P of the hot tile whose K half was just processed
+    for (int j = 0;; ++j) {
+        const int s = j & 1;
+        const int k = s ? kind[1] : kind[0];
+        const int id = s ? uid[1] : uid[0];
+        if (k == kNone) break;
+        unsigned char *slot = ring + s * slot_bytes;
+        {  // wait for this slot's loads: the other slot's are younger
+            const int ky = s ? kind[0] : kind[1];
+            if (ky == kWarm) wait_vm<NLW>();
+            else if (ky == kHotK || ky == kHotV) wait_vm<NLH>();
+            else wait_vm<0>();
+        }
+
+        if (k == kWarm) {
+            // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS;
+            //      the fast paths hold when no -1024 s overflows (K and V scales of the unit)
+            bool kfast, vfast;
+            h2 ksc[16], kng[16], kze[16];
+            {
+                const h2 s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
+                const h2 z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
+                const h2 n2 = s2v * (h2){nmul, nmul};
+                const uint32_t nb = as_u32(n2);
+                kfast = !__builtin_amdgcn_ballot_w64(!finite2(nb));
+                bool vfin = true;
+                if (lane * 4 < L::VMB) {
+                    const h2 vsv = as_h2(*(const uint32_t *)(slot + L::VS + 4 * lane));
+                    const _Float16 n0 = (_Float16)(-1024.0f);
+                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
+                }
+                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
+                uint32_t *kmw = (uint32_t *)kmeta;
+                kmw[(0 * 4 + g2) * 16 + pi2] = as_u32(s2v);
+                kmw[(1 * 4 + g2) * 16 + pi2] = nb;
+                kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
+                __builtin_amdgcn_wave_barrier();
+                const u4 *src = (const u4 *)kmeta;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    const u4 av = src[(0 * 4 + grp) * 4 + q4];
+                    const u4 nv = src[(1 * 4 + grp) * 4 + q4];
+                    const u4 zv = src[(2 * 4 + grp) * 4 + q4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t ae = av[e], ne = nv[e], ze = zv[e];
+                        ksc[4 * q4 + e] = as_h2(ae);
+                        kng[4 * q4 + e] = as_h2(ne);
+                        kze[4 * q4 + e] = as_h2(ze);
+                    }
+                }
+            }
+
+            const int tok0 = id * kUnit;  // first token of the unit (pair-local warm index)
+            // ---- phase 1: QK of both tiles (the K meta dies after it)
+            f4 sc[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t kraw[BK];
+                {
+                    const uint32_t *kp = (const uint32_t *)(slot + k_lane + 16 * h * L::KR);
+#pragma unroll
+                    for (int jj = 0; jj < BK; ++jj) kraw[jj] = kp[jj];
+                }
+                KWin<BK> W;
+                k_windows<BK>(kraw, W);
+                sc[h] = (f4){0.f, 0.f, 0.f, 0.f};
+                if (kfast) {
+#pragma unroll
+                    for (int st = 0; st < KSTEPS; ++st) {
+                        h8 a;
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            const int pi = 4 * st + kk;
+                            const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            h2 v = pk_fma(as_h2(uu), ksc[pi], kng[pi]);
+                            v = v + kze[pi];
+                            a[2 * kk] = v[0];
+                            a[2 * kk + 1] = v[1];
+                        }
+                        sc[h] = mfma_k32(a, qop[st], sc[h]);
+                    }
+                } else {
+#pragma unroll
+                    for (int st = 0; st < KSTEPS; ++st) {
+                        h8 a;
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            const int pi = 4 * st + kk;
+                            const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
+                            const h2 c = as_h2(uu) - (h2){mv, mv};  // the code, exactly
+                            h2 v = c * ksc[pi];
+                            v = v + kze[pi];
+                            a[2 * kk] = v[0];
+                            a[2 * kk + 1] = v[1];
+                        }
+                        sc[h] = mfma_k32(a, qop[st], sc[h]);
+                    }
+                }
+            }
+
+            // ---- phase 2, per tile: V dequant, softmax, PV
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                uint32_t vraw[4];
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    const unsigned char *vp = slot + v_lane + (16 * h + ii) * L::VR;
+                    if (BV == 3) {  // the chunk's 3 bytes from the aligned 8 around them
+                        const uint32_t *vq = (const uint32_t *)(slot + (v_lane & ~3) + (16 * h + ii) * L::VR);
+                        vraw[ii] = __builtin_amdgcn_alignbyte(vq[1], vq[0], v_lane & 3);
+                    } else vraw[ii] = BV == 2 ? lds_u16(vp) : *(const uint32_t *)vp;
+                }
+                h2 vs[2], vz[2];
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) {
+                    const int ta = 16 * h + 2 * pp;  // + 4 grp (in vm_lane)
+                    vs[pp] = lds_h2(slot + L::VS + vm_lane + ta * NG * 2, slot + L::VS + vm_lane + (ta + 1) * NG * 2);
+                    vz[pp] = lds_h2(slot + L::VZ + vm_lane + ta * NG * 2, slot + L::VZ + vm_lane + (ta + 1) * NG * 2);
+                }
+                uint32_t vpair[2][8];
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) {
+                    uint32_t win[VSlot<BV>::NW];
+                    v_windows<BV>(vraw[2 * pp], vraw[2 * pp + 1], win);
+                    if (vfast) {
+                        h2 vn[v_noffs<BV>()];
+#pragma unroll
+                        for (int oi = 0; oi < v_noffs<BV>(); ++oi) {
+                            const _Float16 m = (_Float16)(-magic_val(oi * v_ostep<BV>()));
+                            vn[oi] = vs[pp] * (h2){m, m};
+                        }
+#pragma unroll
+                        for (int kk = 0; kk < 8; ++kk) {
+                            const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                            h2 v = pk_fma(as_h2(uu), vs[pp], vn[voff<BV>(kk) / v_ostep<BV>()]);
+                            v = v + vz[pp];
+                            vpair[pp][kk] = as_u32(v);
+                        }
+                    } else {
+#pragma unroll
+                        for (int kk = 0; kk < 8; ++kk) {
+                            const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                            const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
+                            const h2 c = as_h2(uu) - (h2){mv, mv};
+                            h2 v = c * vs[pp];
+                            v = v + vz[pp];
+                            vpair[pp][kk] = as_u32(v);
+                        }
+                    }
+                }
+
+                // ---- softmax
+                f4 sh = sc[h];
+                const int t0 = tok0 + 16 * h;
+                const int nvalid = min(4, nw - (t0 + 4 * grp));
+                if (t0 + 16 > nw) {
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii)
+                        if (ii >= nvalid) sh[ii] = -INFINITY;
+                }
+                stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sh, sl2, nvalid);
+                const h4 pop = softmax16(stt, sh, sl2);
+
+                // ---- PV
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk)
+                    stt.acc[kk] = mfma_k16(__builtin_bit_cast(h4, (u2){vpair[0][kk], vpair[1][kk]}), pop, stt.acc[kk]);
+            }
+        } else if (k == kHotK) {
+            // ---- hot K tile: 16 tokens x 256 B; lane = (token col, 32 channels of group grp)
+            uint32_t nat[16], pairs[16];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const u4 x = *(const u4 *)(slot + col * 256 + grp * 64 + 16 * q4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t xe = x[e];
+                    nat[4 * q4 + e] = xe;
+                }
+            }
+            hot_k_pairs<BK>(nat, pairs);
+            f4 sh = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < KSTEPS; ++st)
+                sh = mfma_k32(__builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]}),
+                              qop[st], sh);
+            const int t0 = id * 16;
+            const int nvalid = min(4, nh - (t0 + 4 * grp));
+            if (t0 + 16 > nh) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii)
+                    if (ii >= nvalid) sh[ii] = -INFINITY;
+            }
+            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, sl2, nvalid);
+            hot_p = softmax16(stt, sh, sl2);
+        } else {
+            // ---- hot V tile: lane = (chunk col, tokens 4 grp .. +3)
+            u4 w[4];
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) w[ii] = *(const u4 *)(slot + (4 * grp + ii) * 256 + col * 16);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const uint32_t sel = (kk & 1) ? 0x07060302u : 0x05040100u;
+                const uint32_t lo = perm(w[1][kk / 2], w[0][kk / 2], sel);
+                const uint32_t hi = perm(w[3][kk / 2], w[2][kk / 2], sel);
+                stt.acc[kk] = mfma_k16(__builtin_bit_cast(h4, (u2){lo, hi}), hot_p, stt.acc[kk]);
+            }
+        }
+
+        // ---- every read of this slot has landed: refill it
+        wait_lgkm0();
+        __builtin_amdgcn_wave_barrier();
+        if (s) {
+            next_unit(kind[1], uid[1]);
+            issue(kind[1], uid[1], slot);
+        } else {
+            next_unit(kind[0], uid[0]);
+            issue(kind[0], uid[0], slot);
+        }
+    }
+
+    // ---- merge the waves (the ring memory is reused), write the split partial
+    wait_vm<0>();
+    stt.l = wsum16(stt.l);
+    __syncthreads();
+    float *mlds = (float *)smem;                   // [W][16]
+    float *llds = mlds + kWaves * 16;              // [W][16]
+    float *alds = llds + kWaves * 16;              // [W][16][D]
+    if (grp == 0) {
+        mlds[wave * 16 + col] = stt.m2;
+        llds[wave * 16 + col] = stt.l;
+    }
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) alds[(wave * 16 + col) * kD + 8 * (4 * grp + ii) + kk] = stt.acc[kk][ii];
+    __syncthreads();
+    float *part = p.part + ((bh * p.nchunk + chunk) * p.nsplit + split) * (int64_t)(p.prows * (kD + 4));
+    for (int e = threadIdx.x; e < nrows * kD; e += 64 * kWaves) {
+        const int rr = e / kD, ch = e % kD;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, mlds[w * 16 + rr]);
+        float a = 0.f, l = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+            const float mw = mlds[w * 16 + rr];
+            const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
+            a += f * alds[(w * 16 + rr) * kD + ch];
+            l += f * llds[w * 16 + rr];
+        }
+        part[rr * (kD + 4) + 4 + ch] = a;
+        if (ch == 0) {
+            part[rr * (kD + 4) + 0] = mx;
+            part[rr * (kD + 4) + 1] = l;
+        }
+    }
+}
+
+// LDS slot of the fast kernel: one warm unit, or one 16-token hot K or V half.
+int64_t decode_fast_slot_bytes(int kb, int vb, int Gv) {
+    const int NG = kD / Gv;
+    int64_t warm = (int64_t)kUnit * 16 * (kb + vb) + 512 + 128 * NG;
+    int64_t s = warm > 4096 ? warm : 4096;
+    return (s + 255) / 256 * 256;
+}
+// LDS of one workgroup: W waves x (NS slots + K meta scratch) + the work
+// counter; the end-of-split merge reuses it.
+int64_t decode_fast_lds_bytes(int64_t slot) {
+    const int64_t ring = kWaves * (kNS * slot + kKmetaBytes) + 16;
+    const int64_t merge = (int64_t)(2 * kWaves * 16 + kWaves * 16 * kD) * 4;
+    return ring > merge ? ring : merge;
+}
+int decode_fast_waves() { return kWaves; }
+
+bool decode_fast_eligible(const DecodeParams &p, int wk) {
+    return wk == AKV_WARM_AFFINE && p.D == kD && p.T % kUnit == 0 && p.n_out == 0 &&
+           (p.Gv == 32 || p.Gv == 64 || p.Gv == 128);
+}
+
+template <int BK, int BV, int NG>
+static hipError_t launch_fast(const DecodeParams &p, hipStream_t s) {
+    dim3 grid(p.nsplit, p.Hkv, p.B * p.nchunk);
+    const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes);
+    static bool attr_set = false;  // raise the dynamic LDS cap above 64 KiB once
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG>), grid, dim3(64 * kWaves), lds, s, p);
+    return hipGetLastError();
+}
+
+template <int BK, int BV>
+static hipError_t launch_fast_ng(const DecodeParams &p, hipStream_t s) {
+    if (p.Gv == 32) return launch_fast<BK, BV, 4>(p, s);
+    if (p.Gv == 64) return launch_fast<BK, BV, 2>(p, s);
+    if (p.Gv == 128) return launch_fast<BK, BV, 1>(p, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, hipStream_t s) {
+#define AKV_FKV(a, b) \
+    if (kb == a && vb == b) return launch_fast_ng<a, b>(p, s);
+    AKV_FKV(2, 2) AKV_FKV(2, 3) AKV_FKV(2, 4) AKV_FKV(3, 2) AKV_FKV(3, 3) AKV_FKV(3, 4) AKV_FKV(4, 2) AKV_FKV(4, 3)
+    AKV_FKV(4, 4)
+#undef AKV_FKV
+    return hipErrorInvalidValue;
+}
+
+}  // namespace akv
