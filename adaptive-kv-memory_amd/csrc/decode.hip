@@ -701,9 +701,12 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
 // float4 loads in flight, the split lanes are summed through LDS.
 template <int D>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p) {
-    constexpr int NQ = D / 4, SL = 256 / NQ, PS = D + 4;
-    __shared__ float fs[1024];
-    __shared__ float red[4][2];
+    // Thread (split lane sl, channel quad q) walks splits sl, sl + SL, ... in
+    // batches of KB whose loads are all in flight together, merging them
+    // online (log-sum-exp); the SL lanes then merge through LDS.  At <= SL*KB
+    // splits the whole merge costs one round trip to memory.
+    constexpr int NQ = D / 4, SL = 256 / NQ, PS = D + 4, KB = 4;
+    __shared__ float sm[SL], sls[SL];
     __shared__ f4 accl[SL][NQ];
     const int bhc = blockIdx.x, rr = blockIdx.y;
     const int chunk = bhc % p.nchunk;
@@ -714,57 +717,65 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p
     const int ns = p.nsplit;
     const int64_t pstride = (int64_t)p.prows * PS;
     const float *part = p.part + (bh * p.nchunk + chunk) * (int64_t)ns * pstride + rr * PS;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    float mx = -INFINITY;
-    for (int s = tid; s < ns; s += 256) mx = fmaxf(mx, part[s * pstride]);
-    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) red[w][0] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0][0], red[1][0]), fmaxf(red[2][0], red[3][0]));
-    float l = 0.f;
-    for (int s = tid; s < ns; s += 256) {
-        const float ms = part[s * pstride];
-        const float f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
-        if (s < 1024) fs[s] = f;
-        l += f * part[s * pstride + 1];
-    }
-    for (int o = 32; o > 0; o >>= 1) l += __shfl_xor(l, o);
-    if (lane == 0) red[w][1] = l;
-    __syncthreads();
-    const float L = (red[0][1] + red[1][1]) + (red[2][1] + red[3][1]);
-    const int q = tid % NQ, sl = tid / NQ;
-    f4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = a0;
-    int s = sl;
-    for (; s + SL < ns; s += 2 * SL) {
-        const f4 x0 = *(const f4 *)(part + s * pstride + 4 + 4 * q);
-        const f4 x1 = *(const f4 *)(part + (s + SL) * pstride + 4 + 4 * q);
-        const float f0 = s < 1024 ? fs[s] : 0.f, f1 = s + SL < 1024 ? fs[s + SL] : 0.f;
-        a0 += f0 * x0;
-        a1 += f1 * x1;
-    }
-    for (; s < ns; s += SL) {
-        const f4 x0 = *(const f4 *)(part + s * pstride + 4 + 4 * q);
-        a0 += (s < 1024 ? fs[s] : 0.f) * x0;
-    }
-    for (s = 1024 + sl; s < ns; s += SL) {  // more than 1024 splits: factors not cached
-        const float ms = part[s * pstride];
-        const float f = (ms == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
-        a0 += f * *(const f4 *)(part + s * pstride + 4 + 4 * q);
-    }
-    accl[sl][q] = a0 + a1;
-    __syncthreads();
-    if (tid < D) {
-        const int qq = tid / 4, e = tid % 4;
-        float o = 0.f;
+    const int tid = threadIdx.x, q = tid % NQ, sl = tid / NQ;
+    float mx = -INFINITY, l = 0.f;
+    f4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = sl; s0 < ns; s0 += KB * SL) {
+        float ms[KB], ls[KB];
+        f4 xs[KB];
 #pragma unroll
-        for (int k = 0; k < SL; ++k) o += accl[k][qq][e];
-        o = o / L;
+        for (int k = 0; k < KB; ++k) {
+            const int s = s0 + k * SL;
+            if (s < ns) {
+                ms[k] = part[s * pstride];
+                ls[k] = part[s * pstride + 1];
+                xs[k] = *(const f4 *)(part + s * pstride + 4 + 4 * q);
+            } else {
+                ms[k] = -INFINITY;
+                ls[k] = 0.f;
+                xs[k] = (f4){0.f, 0.f, 0.f, 0.f};
+            }
+        }
+        float nm = mx;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) nm = fmaxf(nm, ms[k]);
+        if (nm == -INFINITY) continue;
+        const float fo = (mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mx - nm);
+        a *= fo;
+        l *= fo;
+#pragma unroll
+        for (int k = 0; k < KB; ++k) {
+            const float f = (ms[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[k] - nm);
+            a += f * xs[k];
+            l += f * ls[k];
+        }
+        mx = nm;
+    }
+    if (q == 0) {
+        sm[sl] = mx;
+        sls[sl] = l;
+    }
+    accl[sl][q] = a;
+    __syncthreads();
+    if (tid < NQ) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int k = 0; k < SL; ++k) M = fmaxf(M, sm[k]);
+        f4 o = {0.f, 0.f, 0.f, 0.f};
+        float L = 0.f;
+#pragma unroll
+        for (int k = 0; k < SL; ++k) {
+            const float f = (sm[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(sm[k] - M);
+            o += f * accl[k][tid];
+            L += f * sls[k];
+        }
         const int r = row0 + rr;
         const int h = kvh * p.g + r / p.M, m = r % p.M;
         const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
-        p.out[row * D + tid] = (_Float16)o;
+        const h4 ov = {(_Float16)(o[0] / L), (_Float16)(o[1] / L), (_Float16)(o[2] / L), (_Float16)(o[3] / L)};
+        *(h4 *)(p.out + row * D + 4 * tid) = ov;
         if (tid == 0 && p.rowstats) {
-            p.rowstats[2 * row] = mx;
+            p.rowstats[2 * row] = M;
             p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
         }
     }

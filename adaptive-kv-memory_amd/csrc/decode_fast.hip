@@ -30,8 +30,12 @@
 //        enter PV as fp16 scaled by 2^7.
 //   PV:  O^T[16 chunks x 16 rows] += V^T . P^T, 8 x v_mfma_f32_16x16x16_f16.
 //        Lane (chunk l%16 of 8 channels, tokens 4(l/16)..+3) pairs two tokens
-//        per dword with byte permutes and shifts, then the same exact
-//        and-or / fma / add dequant with the token's (s, z) of its group.
+//        per dword with byte permutes and shifts; one and-or and one packed
+//        fma give round16(c*s) with the token's scale of its group.  The
+//        zero-points enter through one more MFMA per tile that accumulates
+//        sum_t P * z(token, group), added to every channel of the group at
+//        the end (so V skips the second fp16 rounding of the reference's
+//        dequant: the output stays within the attention tolerance).
 // The 4 waves merge in LDS and write one (m, l, acc) partial per workgroup;
 // decode_reduce_kernel merges the splits.
 //
@@ -48,7 +52,8 @@ namespace {
 constexpr int kD = 128;
 constexpr int kWaves = 12;           // waves per workgroup (one workgroup per CU, 3 per SIMD)
 constexpr int kUnit = 32;            // warm tokens per ring slot
-constexpr int kNS = 2;               // ring slots per wave
+constexpr int kNS = 2;               // ring slots per wave (deeper rings only lengthen the tail)
+constexpr int kLdsCap = 160 * 1024;  // LDS of one CU
 constexpr int kKmetaBytes = 3 * 4 * 16 * 4;  // [s | n | z][group][pair] u32
 constexpr int kHotLoads = 4;         // 16 tokens x 256 B = 4 KiB = 4 wave loads
 constexpr float kThreshF = 8.0f;
@@ -267,7 +272,8 @@ __device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, i
 
 struct Soft {
     float m2, l;
-    f4 acc[8];
+    f4 acc[8];  // O^T: channel 8*chunk + j of chunk 4*grp + i, row col
+    f4 accz;    // sum_t P * (V zero-point of the chunk's group): added to every channel of the chunk at the end
 };
 
 // Online softmax over one 16-token tile.  s: raw q.k of tokens 4*grp+i for
@@ -285,6 +291,7 @@ __device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
         st.l *= alpha;
 #pragma unroll
         for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
+        st.accz *= alpha;
         st.m2 = mn;
     }
     const float bias = kPLog2F - st.m2;
@@ -334,9 +341,22 @@ __device__ __forceinline__ void hot_k_pairs(const uint32_t *nat, uint32_t *pairs
 #ifndef AKV_FAST_WAVES_PER_EU
 #define AKV_FAST_WAVES_PER_EU 3
 #endif
-template <int BK, int BV, int NG>
+// Loads still in flight behind the oldest ring slot, given how many of the
+// younger slots hold a warm unit (nw) or a hot half (nh); nw + nh <= 2.
+template <int NLW, int NLH>
+__device__ __forceinline__ void wait_younger(int nw, int nh) {
+    if (nw == 2) wait_vm<2 * NLW>();
+    else if (nw == 1 && nh == 1) wait_vm<NLW + NLH>();
+    else if (nw == 1) wait_vm<NLW>();
+    else if (nh == 2) wait_vm<2 * NLH>();
+    else if (nh == 1) wait_vm<NLH>();
+    else wait_vm<0>();
+}
+
+template <int BK, int BV, int NG, int NS>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(AKV_FAST_WAVES_PER_EU, AKV_FAST_WAVES_PER_EU)))
 void decode_fast_kernel(const DecodeParams p) {
+    static_assert(NS == 2 || NS == 3, "ring depth");
     using L = WarmLayout<BK, BV, NG>;
     constexpr int KSTEPS = kD / 32;
     constexpr int NLW = L::NLOAD;     // loads of a warm unit
@@ -352,9 +372,9 @@ void decode_fast_kernel(const DecodeParams p) {
     const int row0 = chunk * 16;
     const int nrows = min(16, p.R - row0);
     const int slot_bytes = p.slot_bytes;
-    unsigned char *ring = smem + wave * (kNS * slot_bytes + kKmetaBytes);
-    unsigned char *kmeta = ring + kNS * slot_bytes;
-    unsigned *work = (unsigned *)(smem + kWaves * (kNS * slot_bytes + kKmetaBytes));
+    unsigned char *ring = smem + wave * (NS * slot_bytes + kKmetaBytes);
+    unsigned char *kmeta = ring + NS * slot_bytes;
+    unsigned *work = (unsigned *)(smem + kWaves * (NS * slot_bytes + kKmetaBytes));  // item counter
 
     const int r = row0 + col;
     const int row_valid = col < nrows;
@@ -380,18 +400,22 @@ void decode_fast_kernel(const DecodeParams p) {
     // order the warm code pairs come out in (hot K is permuted to match)
     h8 qop[KSTEPS];
     {
-        const _Float16 *qrow = p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp;
+        const u4 *qrow = (const u4 *)(p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp);
+        uint32_t nat[16], pairs[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const u4 x = qrow[q4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t xe = x[e];
+                nat[4 * q4 + e] = xe;
+            }
+        }
+        hot_k_pairs<BK>(nat, pairs);
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qop[st][j] = qrow[kpair_chan<BK>(4 * st + j / 2, j % 2)];
+            qop[st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
     }
-
-    Soft stt;
-    stt.m2 = -INFINITY;
-    stt.l = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) stt.acc[j] = (f4){0.f, 0.f, 0.f, 0.f};
 
     WarmRes R;
     {
@@ -406,25 +430,8 @@ void decode_fast_kernel(const DecodeParams p) {
     const u4 rkh = rsrc4(p.khot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
     const u4 rvh = rsrc4(p.vhot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
 
-    Masks<BK> km;
-    km.init();
-    Masks<BV> vmk;
-    if (BV == BK) vmk = *(const Masks<BV> *)&km;
-    else vmk.init();
-    // K meta prep role of this lane: (group g2, pair pi2)
-    const int g2 = lane >> 4, pi2 = lane & 15;
-    const int kch_lo = 32 * g2 + kpair_chan<BK>(pi2, 0), kch_hi = 32 * g2 + kpair_chan<BK>(pi2, 1);
-    const _Float16 nmul = (_Float16)(-magic_val(koff<BK>(pi2)));
-    // V role: chunk col and its group; lane parts of the slot offsets
-    const int gv = (8 * col) / GV;
-    const int k_lane = L::KC + col * L::KR + grp * 4 * BK;
-    const int v_lane = L::VC + 4 * grp * L::VR + (BV == 3 ? 3 * col : BV == 4 ? 4 * col : 2 * col);
-    const int vm_lane = (4 * grp * NG + gv) * 2;
-
-    __syncthreads();  // work counter initialised
-
-    // ---- the ring: slot s holds unit (kind[s], id[s]); a hot item is two units (K, then V)
-    int kind[kNS], uid[kNS];
+    // ---- the ring: a queue of NS slots, oldest first; a hot item is two units (K, then V)
+    int qk[NS], qi[NS];
     int pend = -1;  // hot tile whose V half is still to be issued
     auto next_unit = [&](int &k, int &id) {
         if (pend >= 0) {
@@ -453,24 +460,52 @@ void decode_fast_kernel(const DecodeParams p) {
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
+    __syncthreads();
 #pragma unroll
-    for (int s2 = 0; s2 < kNS; ++s2) {
-        next_unit(kind[s2], uid[s2]);
-        issue(kind[s2], uid[s2], ring + s2 * slot_bytes);
+    for (int s2 = 0; s2 < NS; ++s2) {
+        next_unit(qk[s2], qi[s2]);
+        issue(qk[s2], qi[s2], ring + s2 * slot_bytes);
     }
 
+    Soft stt;
+    stt.m2 = -INFINITY;
+    stt.l = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) stt.acc[j] = (f4){0.f, 0.f, 0.f, 0.f};
+    stt.accz = (f4){0.f, 0.f, 0.f, 0.f};
+
+    Masks<BK> km;
+    km.init();
+    Masks<BV> vmk;
+    if (BV == BK) vmk = *(const Masks<BV> *)&km;
+    else vmk.init();
+    // K meta prep role of this lane: (group g2, pair pi2)
+    const int g2 = lane >> 4, pi2 = lane & 15;
+    const int kch_lo = 32 * g2 + kpair_chan<BK>(pi2, 0), kch_hi = 32 * g2 + kpair_chan<BK>(pi2, 1);
+    const _Float16 nmul = (_Float16)(-magic_val(koff<BK>(pi2)));
+    // V role: chunk col and its group; lane parts of the slot offsets
+    const int gv = (8 * col) / GV;
+    const int k_lane = L::KC + col * L::KR + grp * 4 * BK;
+    const int v_lane = L::VC + 4 * grp * L::VR + (BV == 3 ? 3 * col : BV == 4 ? 4 * col : 2 * col);
+    const int vm_lane = (4 * grp * NG + gv) * 2;
+
+    __syncthreads();  // item counter initialised
+
     h4 hot_p = {};  // P of the hot tile whose K half was just processed
-    for (int j = 0;; ++j) {
-        const int s = j & 1;
-        const int k = s ? kind[1] : kind[0];
-        const int id = s ? uid[1] : uid[0];
+    int head = 0;  // ring slot of the oldest queue entry
+    for (;;) {
+        const int k = qk[0];
+        const int id = qi[0];
         if (k == kNone) break;
-        unsigned char *slot = ring + s * slot_bytes;
-        {  // wait for this slot's loads: the other slot's are younger
-            const int ky = s ? kind[0] : kind[1];
-            if (ky == kWarm) wait_vm<NLW>();
-            else if (ky == kHotK || ky == kHotV) wait_vm<NLH>();
-            else wait_vm<0>();
+        unsigned char *slot = ring + head * slot_bytes;
+        {  // wait for this slot's loads: the younger slots' loads may stay in flight
+            int nwy = 0, nhy = 0;
+#pragma unroll
+            for (int i = 1; i < NS; ++i) {
+                nwy += qk[i] == kWarm;
+                nhy += qk[i] == kHotK || qk[i] == kHotV;
+            }
+            wait_younger<NLW, NLH>(nwy, nhy);
         }
 
         if (k == kWarm) {
@@ -596,7 +631,6 @@ void decode_fast_kernel(const DecodeParams p) {
                         for (int kk = 0; kk < 8; ++kk) {
                             const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
                             h2 v = pk_fma(as_h2(uu), vs[pp], vn[voff<BV>(kk) / v_ostep<BV>()]);
-                            v = v + vz[pp];
                             vpair[pp][kk] = as_u32(v);
                         }
                     } else {
@@ -606,7 +640,6 @@ void decode_fast_kernel(const DecodeParams p) {
                             const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
                             const h2 c = as_h2(uu) - (h2){mv, mv};
                             h2 v = c * vs[pp];
-                            v = v + vz[pp];
                             vpair[pp][kk] = as_u32(v);
                         }
                     }
@@ -628,6 +661,7 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk)
                     stt.acc[kk] = mfma_k16(__builtin_bit_cast(h4, (u2){vpair[0][kk], vpair[1][kk]}), pop, stt.acc[kk]);
+                stt.accz = mfma_k16(__builtin_bit_cast(h4, (u2){as_u32(vz[0]), as_u32(vz[1])}), pop, stt.accz);
             }
         } else if (k == kHotK) {
             // ---- hot K tile: 16 tokens x 256 B; lane = (token col, 32 channels of group grp)
@@ -670,19 +704,20 @@ void decode_fast_kernel(const DecodeParams p) {
             }
         }
 
-        // ---- every read of this slot has landed: refill it
+        // ---- every read of this slot has landed: refill it with the youngest entry
         wait_lgkm0();
         __builtin_amdgcn_wave_barrier();
-        if (s) {
-            next_unit(kind[1], uid[1]);
-            issue(kind[1], uid[1], slot);
-        } else {
-            next_unit(kind[0], uid[0]);
-            issue(kind[0], uid[0], slot);
+#pragma unroll
+        for (int i = 0; i + 1 < NS; ++i) {
+            qk[i] = qk[i + 1];
+            qi[i] = qi[i + 1];
         }
+        next_unit(qk[NS - 1], qi[NS - 1]);
+        issue(qk[NS - 1], qi[NS - 1], slot);
+        head = head + 1 == NS ? 0 : head + 1;
     }
 
-    // ---- merge the waves (the ring memory is reused), write the split partial
+    // ---- merge the waves (the ring memory is reused)
     wait_vm<0>();
     stt.l = wsum16(stt.l);
     __syncthreads();
@@ -696,7 +731,7 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) alds[(wave * 16 + col) * kD + 8 * (4 * grp + ii) + kk] = stt.acc[kk][ii];
+        for (int ii = 0; ii < 4; ++ii) alds[(wave * 16 + col) * kD + 8 * (4 * grp + ii) + kk] = stt.acc[kk][ii] + stt.accz[ii];
     __syncthreads();
     float *part = p.part + ((bh * p.nchunk + chunk) * p.nsplit + split) * (int64_t)(p.prows * (kD + 4));
     for (int e = threadIdx.x; e < nrows * kD; e += 64 * kWaves) {
@@ -727,8 +762,8 @@ int64_t decode_fast_slot_bytes(int kb, int vb, int Gv) {
     int64_t s = warm > 4096 ? warm : 4096;
     return (s + 255) / 256 * 256;
 }
-// LDS of one workgroup: W waves x (NS slots + K meta scratch) + the work
-// counter; the end-of-split merge reuses it.
+// LDS of one workgroup: W waves x (NS slots + K meta scratch) + the item
+// counter; the end-of-split merge reuses the rings.
 int64_t decode_fast_lds_bytes(int64_t slot) {
     const int64_t ring = kWaves * (kNS * slot + kKmetaBytes) + 16;
     const int64_t merge = (int64_t)(2 * kWaves * 16 + kWaves * 16 * kD) * 4;
@@ -741,19 +776,24 @@ bool decode_fast_eligible(const DecodeParams &p, int wk) {
            (p.Gv == 32 || p.Gv == 64 || p.Gv == 128);
 }
 
-template <int BK, int BV, int NG>
-static hipError_t launch_fast(const DecodeParams &p, hipStream_t s) {
+template <int BK, int BV, int NG, int NS>
+static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
     dim3 grid(p.nsplit, p.Hkv, p.B * p.nchunk);
     const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes);
     static bool attr_set = false;  // raise the dynamic LDS cap above 64 KiB once
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCap);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG>), grid, dim3(64 * kWaves), lds, s, p);
+    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG, NS>), grid, dim3(64 * kWaves), lds, s, p);
     return hipGetLastError();
+}
+
+template <int BK, int BV, int NG>
+static hipError_t launch_fast(const DecodeParams &p, hipStream_t s) {
+    return launch_fast_ns<BK, BV, NG, kNS>(p, s);
 }
 
 template <int BK, int BV>
