@@ -395,27 +395,7 @@ void decode_fast_kernel(const DecodeParams p) {
     const int n_items = (h_end > h_begin ? n_ht : 0) + (w_end > w_begin ? n_wu : 0);
     const int n_hot_items = h_end > h_begin ? n_ht : 0;
     if (threadIdx.x == 0) *work = 0u;
-
-    // Q operand (B of QK): lane = (row col, channel group grp), in the channel
-    // order the warm code pairs come out in (hot K is permuted to match)
-    h8 qop[KSTEPS];
-    {
-        const u4 *qrow = (const u4 *)(p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp);
-        uint32_t nat[16], pairs[16];
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const u4 x = qrow[q4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t xe = x[e];
-                nat[4 * q4 + e] = xe;
-            }
-        }
-        hot_k_pairs<BK>(nat, pairs);
-#pragma unroll
-        for (int st = 0; st < KSTEPS; ++st)
-            qop[st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
-    }
+    __syncthreads();  // item counter initialised before any wave takes an item
 
     WarmRes R;
     {
@@ -460,12 +440,36 @@ void decode_fast_kernel(const DecodeParams p) {
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
-    __syncthreads();
+    // Only the first slot is filled up front: every wave's first unit is in
+    // the memory queue before any wave's second, so compute starts as soon as
+    // a first unit lands; the other slots fill once it has (loop, first pass).
+    next_unit(qk[0], qi[0]);
+    issue(qk[0], qi[0], ring);
 #pragma unroll
-    for (int s2 = 0; s2 < NS; ++s2) {
-        next_unit(qk[s2], qi[s2]);
-        issue(qk[s2], qi[s2], ring + s2 * slot_bytes);
+    for (int s2 = 1; s2 < NS; ++s2) qk[s2] = kNone;
+    bool primed = false;
+
+    // Q operand (B of QK): lane = (row col, channel group grp), in the channel
+    // order the warm code pairs come out in (hot K is permuted to match)
+    h8 qop[KSTEPS];
+    {
+        const u4 *qrow = (const u4 *)(p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp);
+        uint32_t nat[16], pairs[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const u4 x = qrow[q4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t xe = x[e];
+                nat[4 * q4 + e] = xe;
+            }
+        }
+        hot_k_pairs<BK>(nat, pairs);
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st)
+            qop[st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
     }
+
 
     Soft stt;
     stt.m2 = -INFINITY;
@@ -489,8 +493,6 @@ void decode_fast_kernel(const DecodeParams p) {
     const int v_lane = L::VC + 4 * grp * L::VR + (BV == 3 ? 3 * col : BV == 4 ? 4 * col : 2 * col);
     const int vm_lane = (4 * grp * NG + gv) * 2;
 
-    __syncthreads();  // item counter initialised
-
     h4 hot_p = {};  // P of the hot tile whose K half was just processed
     int head = 0;  // ring slot of the oldest queue entry
     for (;;) {
@@ -506,6 +508,14 @@ void decode_fast_kernel(const DecodeParams p) {
                 nhy += qk[i] == kHotK || qk[i] == kHotV;
             }
             wait_younger<NLW, NLH>(nwy, nhy);
+        }
+        if (!primed) {
+            primed = true;
+#pragma unroll
+            for (int s2 = 1; s2 < NS; ++s2) {
+                next_unit(qk[s2], qi[s2]);
+                issue(qk[s2], qi[s2], ring + s2 * slot_bytes);
+            }
         }
 
         if (k == kWarm) {
