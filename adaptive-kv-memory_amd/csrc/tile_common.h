@@ -1,0 +1,242 @@
+// Device helpers shared by the LDS-tiled attention kernels over the
+// block-affine warm tier (decode_fast.hip, prefill.hip): buffer loads into
+// LDS, exact fp16 dequant of packed code pairs and the code windows of each
+// bit width, the hot-K channel permutation, and the online softmax of one
+// 16-token MFMA tile.
+#pragma once
+
+#include "akv_common.h"
+
+namespace akv {
+namespace {
+
+constexpr float kThreshF = 8.0f;
+constexpr float kPLog2F = 7.0f;
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+// Buffer resource as four scalars (raw buffer, no stride, range-checked to `bytes`).
+__device__ __forceinline__ u4 rsrc4(const void *base, uint32_t bytes) {
+    const uint64_t b = (uint64_t)base;
+    return (u4){(uint32_t)b, (uint32_t)(b >> 32) & 0xFFFFu, bytes, (uint32_t)kRsrcWord3};
+}
+
+// One LDS-DMA instruction: for each lane i set in `mask`, 16 bytes at buffer
+// offset soff + voff_i are written to LDS [lds + 16 i]; bytes past the
+// resource range arrive as zeros.  Written as one asm block so the compiler
+// can neither merge two of them under divergent control flow nor change how
+// many are issued (the vmcnt waits count them); M0 is restored afterwards.
+__device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff, uint64_t mask) {
+    uint64_t saved;
+    uint32_t saved_m0;
+    asm volatile(
+        "s_mov_b32 %[sm0], m0\n\t"
+        "s_mov_b32 m0, %[lds]\n\t"
+        "s_mov_b64 %[sv], exec\n\t"
+        "s_and_b64 exec, exec, %[mask]\n\t"
+        "s_nop 0\n\t"
+        "buffer_load_dwordx4 %[voff], %[rsrc], %[soff] offen lds\n\t"
+        "s_mov_b64 exec, %[sv]\n\t"
+        "s_mov_b32 m0, %[sm0]"
+        : [sv] "=&s"(saved), [sm0] "=&s"(saved_m0)
+        : [lds] "s"(lds), [mask] "s"(mask), [voff] "v"(voff), [rsrc] "s"(rsrc), [soff] "s"(soff)
+        : "memory");
+}
+__device__ __forceinline__ uint64_t lane_mask(int bytes) {  // lanes covering `bytes` (>= 16)
+    return bytes >= 1024 ? ~0ull : ((1ull << (bytes >> 4)) - 1ull);
+}
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char *p) { return (uint32_t)(uintptr_t)p; }
+
+// A value the compiler must keep in a VGPR (not rematerialize as a literal),
+// so (x & m) | c selects one v_and_or_b32 with m in a VGPR and c in an SGPR.
+__device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
+    asm volatile("" : "+v"(x));
+    return x;
+}
+
+__device__ __forceinline__ h2 pk_fma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
+
+__device__ __forceinline__ float wmax16(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+__device__ __forceinline__ float wsum16(float x) {
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
+
+// fp16 bits of 2^(10-o): a code at bit offset o of that number's mantissa reads as 2^(10-o) + c.
+__host__ __device__ constexpr uint32_t magic_of(int o) { return (uint32_t)(25 - o) << 10; }
+__host__ __device__ constexpr uint32_t magic2(int o) { return magic_of(o) * 0x00010001u; }
+__host__ __device__ constexpr float magic_val(int o) { return (float)(1 << (10 - o)); }
+
+// --------------------------------------------------------------- K windows
+// Pair pi (0..15) of a lane's 32 channels: window dword and bit offset; the
+// channels (relative to the lane's group) of its halves are kpair_chan().
+template <int BK>
+__host__ __device__ constexpr int koff(int pi) {
+    return BK == 3 ? ((pi % 8) == 0 ? 0 : (pi % 8) == 1 ? 3 : (pi % 8) == 2 ? 6 : (pi % 8) == 3 ? 1
+                      : (pi % 8) == 4 ? 4 : (pi % 8) == 5 ? 7 : (pi % 8) == 6 ? 2 : 5)
+         : BK == 4 ? (pi % 2) * 4
+                   : 2 * (pi % 4);
+}
+template <int BK>
+struct KWin {
+    uint32_t w[BK == 3 ? 6 : (BK == 4 ? 8 : 4)];
+};
+// r: the lane's raw code bytes (BK*4 bytes) as little-endian dwords
+template <int BK>
+__device__ __forceinline__ void k_windows(const uint32_t *r, KWin<BK> &W) {
+    if (BK == 3) {
+        W.w[0] = perm(r[1], r[0], 0x04050102u);
+        W.w[1] = perm(r[1], r[0], 0x03040001u);
+        W.w[2] = perm(r[1], r[0], 0x0C030C00u);
+        W.w[3] = perm(r[2], r[1], 0x06070304u);
+        W.w[4] = perm(r[2], r[1], 0x05060203u);
+        W.w[5] = perm(r[2], r[1], 0x0C050C02u);
+    } else if (BK == 4) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            W.w[2 * d] = r[d];
+            W.w[2 * d + 1] = perm(0u, r[d], 0x0C030C01u);
+        }
+    } else {
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            W.w[2 * d] = r[d];
+            W.w[2 * d + 1] = perm(0u, r[d], 0x0C030C01u);
+        }
+    }
+}
+template <int BK>
+__device__ __forceinline__ uint32_t k_window_of(const KWin<BK> &W, int pi) {
+    if (BK == 3) {
+        const int k = pi % 8, base = 3 * (pi / 8);
+        return W.w[base + (k < 3 ? 0 : (k < 6 ? 1 : 2))];
+    } else if (BK == 4) {
+        return W.w[2 * (pi / 4) + ((pi % 4) >= 2 ? 1 : 0)];
+    } else {
+        return W.w[2 * (pi / 8) + ((pi % 8) >= 4 ? 1 : 0)];
+    }
+}
+
+// --------------------------------------------------------------- V windows
+// One token pair (a, b) of an 8-channel chunk.  da / db: the chunk's bytes
+// of each token at byte 0 of a dword (memory order).  Code k (channel k of
+// the chunk) sits in window vwin(k) at bit offset voff(k), in both halves.
+template <int BV>
+struct VSlot {
+    static constexpr int NW = BV == 3 ? 3 : (BV == 4 ? 4 : 2);
+};
+template <int BV>
+__host__ __device__ constexpr int vwin(int k) {
+    // 3-bit: codes 7,6,5 in window 0; 4,3,2 in 1; 1,0 in 2
+    // 4-bit: ch1,ch0 in 0; ch3,ch2 in 1; ch5,ch4 in 2; ch7,ch6 in 3
+    // 2-bit: codes 3..0 in 0; 7..4 in 1
+    return BV == 3 ? (k >= 5 ? 0 : (k >= 2 ? 1 : 2)) : BV == 4 ? (k / 2) : (k / 4);
+}
+template <int BV>
+__host__ __device__ constexpr int voff(int k) {
+    return BV == 3 ? (k >= 5 ? 3 * (7 - k) : (k >= 2 ? 3 * (4 - k) : 3 * (1 - k)))
+         : BV == 4 ? ((k & 1) ? 0 : 4)
+                   : 2 * (3 - (k & 3));
+}
+template <int BV>
+__device__ __forceinline__ void v_windows(uint32_t da, uint32_t db, uint32_t *win) {
+    if (BV == 3) {
+        win[0] = perm(db, da, 0x05060102u);            // [a.x2 a.x1 | b.x2 b.x1]: W bits 0-15
+        const uint32_t w1 = perm(db, da, 0x04050001u); // [a.x1 a.x0 | b.x1 b.x0]: W bits 8-23
+        win[1] = w1 >> 1;
+        win[2] = w1 >> 10;
+    } else if (BV == 4) {
+        const uint32_t lo = perm(db, da, 0x05040100u); // bytes 0,1 of a | of b
+        const uint32_t hi = perm(db, da, 0x07060302u); // bytes 2,3
+        win[0] = lo;
+        win[1] = lo >> 8;
+        win[2] = hi;
+        win[3] = hi >> 8;
+    } else {
+        const uint32_t w = perm(db, da, 0x05040100u);  // bytes 0,1 of a | of b
+        win[0] = w;
+        win[1] = w >> 8;
+    }
+}
+template <int BV>
+__host__ __device__ constexpr int v_ostep() { return BV == 3 ? 3 : (BV == 4 ? 4 : 2); }
+template <int BV>
+__host__ __device__ constexpr int v_noffs() { return BV == 3 ? 3 : (BV == 4 ? 2 : 4); }
+
+// Masks of a code at bit offset o (both halves), one VGPR per offset 0..7.
+template <int B>
+struct Masks {
+    uint32_t m[8];
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int o = 0; o < 8; ++o) m[o] = in_vgpr((((1u << B) - 1u) << o) * 0x00010001u);
+    }
+};
+
+// --------------------------------------------------------------- layouts
+struct Soft {
+    float m2, l;
+    f4 acc[8];  // O^T: channel 8*chunk + j of chunk 4*grp + i, row col
+    f4 accz;    // sum_t P * (V zero-point of the chunk's group): added to every channel of the chunk at the end
+};
+
+// Online softmax over one 16-token tile.  s: raw q.k of tokens 4*grp+i for
+// row col.  The running max of a row only moves when some score exceeds it by
+// more than 2^8 (log2 units); the test needs no cross-lane traffic, since a
+// row's tile max passes the bound iff one of its four lanes' maxima does.  On
+// the rare update the four lanes of a row agree on the new max through two
+// shuffles.  Returns the fp16 P^T operand (x 2^7).
+__device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
+    const float t = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])) * sl2;
+    if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
+        const float tm2 = wmax16(t);
+        const float mn = fmaxf(st.m2, tm2);
+        const float alpha = __builtin_amdgcn_exp2f(st.m2 - mn);
+        st.l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
+        st.accz *= alpha;
+        st.m2 = mn;
+    }
+    const float bias = kPLog2F - st.m2;
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[i], sl2, bias));
+    st.l += (p[0] + p[1]) + (p[2] + p[3]);
+    return (h4){(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+}
+
+__device__ __forceinline__ uint32_t lds_u16(const unsigned char *p) { return *(const uint16_t *)p; }
+__device__ __forceinline__ h2 lds_h2(const unsigned char *a, const unsigned char *b) {
+    return (h2){*(const _Float16 *)a, *(const _Float16 *)b};
+}
+__device__ __forceinline__ bool finite2(uint32_t x) {
+    return ((x & 0x7C00u) != 0x7C00u) && ((x & 0x7C000000u) != 0x7C000000u);
+}
+
+}  // namespace
+
+// Natural-order hot K (16 dwords of channel pairs 2d, 2d+1 of the lane's 32
+// channels) -> the warm pair order: pair pi holds channels kpair_chan(pi, 0/1),
+// which always have the same parity, so one byte permute builds each pair.
+template <int BK>
+__device__ __forceinline__ void hot_k_pairs(const uint32_t *nat, uint32_t *pairs) {
+#pragma unroll
+    for (int pi = 0; pi < 16; ++pi) {
+        const int c0 = kpair_chan<BK>(pi, 0), c1 = kpair_chan<BK>(pi, 1);
+        const uint32_t sel = (c0 & 1) ? 0x07060302u : 0x05040100u;
+        pairs[pi] = perm(nat[c1 >> 1], nat[c0 >> 1], sel);
+    }
+}
+
+}  // namespace akv
