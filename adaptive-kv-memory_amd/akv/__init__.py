@@ -17,7 +17,7 @@ from .triton_ops import (
     fused_mixed_precision_attention,
     fused_quantized_attention,
 )
-from .warm_tier import WarmTier, decode_attention, dequantize, quantize_kv
+from .warm_tier import WarmTier, decode_attention, dequantize, prefill_attention, quantize_kv
 
 __version__ = "0.1.0"
 
@@ -29,5 +29,5 @@ __all__ = [
     "KVQuantizer", "QuantConfig", "QuantizedTensor",
     "fused_decode_attention", "fused_quantize_evict",
     "HAS_TRITON", "fused_importance_update", "fused_mixed_precision_attention", "fused_quantized_attention",
-    "WarmTier", "decode_attention", "dequantize", "quantize_kv",
+    "WarmTier", "decode_attention", "dequantize", "prefill_attention", "quantize_kv",
 ]

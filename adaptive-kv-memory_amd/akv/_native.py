@@ -66,6 +66,19 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class PrefillArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", _i32), ("B", _i32), ("Hq", _i32), ("Hkv", _i32), ("M", _i32), ("D", _i32),
+        ("q_dtype", _i32),
+        ("q", _vp), ("k_hot", _vp), ("v_hot", _vp),
+        ("n_hot", _i64),
+        ("sm_scale", ctypes.c_float), ("num_splits", _i32),
+        ("warm", WarmDesc),
+        ("out", _vp),
+        ("workspace", _vp), ("workspace_bytes", _i64),
+    ]
+
+
 class QuantArgs(ctypes.Structure):
     _fields_ = [
         ("abi_version", _i32), ("B", _i32), ("H", _i32), ("D", _i32),
@@ -104,8 +117,9 @@ EXPORTS = (
     "akv_decode_workspace_bytes", "akv_decode_attn",
     "akv_quant_pack", "akv_dequant_unpack",
     "akv_bitpack", "akv_bitunpack", "akv_importance_update",
+    "akv_prefill_workspace_bytes", "akv_prefill_attn",
 )
-STRUCTS = (WarmDesc, DecodeArgs, QuantArgs, DequantArgs, ImportanceArgs)
+STRUCTS = (WarmDesc, DecodeArgs, QuantArgs, DequantArgs, ImportanceArgs, PrefillArgs)
 
 _lib: Optional[ctypes.CDLL] = None
 
@@ -138,6 +152,10 @@ def load() -> ctypes.CDLL:
     lib.akv_bitunpack.argtypes = [_vp, _vp, _i64, _i32, _i32, _i32, _vp]
     lib.akv_importance_update.restype = ctypes.c_int
     lib.akv_importance_update.argtypes = [ctypes.POINTER(ImportanceArgs), _vp]
+    lib.akv_prefill_workspace_bytes.restype = _i64
+    lib.akv_prefill_workspace_bytes.argtypes = [ctypes.POINTER(PrefillArgs)]
+    lib.akv_prefill_attn.restype = ctypes.c_int
+    lib.akv_prefill_attn.argtypes = [ctypes.POINTER(PrefillArgs), _vp]
     if lib.akv_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH} has ABI {lib.akv_abi_version()}, expected {ABI_VERSION}")
     for i, st in enumerate(STRUCTS):

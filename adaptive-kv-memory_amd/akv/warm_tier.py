@@ -251,6 +251,48 @@ def decode_attention(q: torch.Tensor, k_hot: Optional[torch.Tensor], v_hot: Opti
     return (out, attn) if return_weights else out
 
 
+def prefill_attention(q: torch.Tensor, k_hot: Optional[torch.Tensor], v_hot: Optional[torch.Tensor],
+                      warm: Optional[WarmTier], sm_scale: Optional[float] = None,
+                      num_splits: int = 0) -> torch.Tensor:
+    """Chunked-prefill attention: q (B, Hq, M, D) fp16 or bf16 -- M positions
+    after every cached token, so no mask over the cache -- over hot fp16
+    (B, Hkv, Nh, D) and the packed warm tier; returns (B, Hq, M, D) in q's
+    dtype.  No attention weights (the M x N matrix is never formed)."""
+    lib = nat.load()
+    nat.require_device(q, k_hot, v_hot)
+    if q.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError("prefill takes float16 or bfloat16 queries")
+    q = nat.dev_contig(q)
+    B, Hq, M, D = q.shape
+    k_hot, v_hot, n_hot = _hot_ptrs(k_hot, v_hot, q.new_empty(0, dtype=torch.float16))
+    Hkv = warm.heads if warm is not None else k_hot.shape[1]
+    out = torch.empty_like(q)
+    a = nat.PrefillArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.B, a.Hq, a.Hkv, a.M, a.D = B, Hq, Hkv, M, D
+    a.q_dtype = nat.dtype_code(q.dtype)
+    a.q = q.data_ptr()
+    if n_hot:
+        a.k_hot, a.v_hot = k_hot.data_ptr(), v_hot.data_ptr()
+    a.n_hot = n_hot
+    a.sm_scale = nat.default_sm_scale(D) if sm_scale is None else float(sm_scale)
+    if warm is not None:
+        a.warm = warm.desc()
+    else:
+        a.warm.kind = nat.WARM_NONE
+    a.out = out.data_ptr()
+    a.num_splits = int(num_splits)
+    nbytes = lib.akv_prefill_workspace_bytes(ctypes.byref(a))
+    if nbytes < 0:
+        nat.check(lib.akv_prefill_attn(ctypes.byref(a), None), "prefill_attention")
+    ws = nat.workspace(nbytes, q.device) if nbytes > 0 else None
+    if ws is not None:
+        a.workspace = ws.data_ptr()
+        a.workspace_bytes = ws.numel()
+    nat.check(lib.akv_prefill_attn(ctypes.byref(a), nat.stream_of(q)), "prefill_attention")
+    return out
+
+
 class DecodeCall:
     """A prepared ``akv_decode_attn`` call on fixed device tensors.
 

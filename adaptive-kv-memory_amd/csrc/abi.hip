@@ -7,6 +7,7 @@
 
 #include "akv_common.h"
 #include "decode.h"
+#include "prefill.h"
 #include "misc.h"
 #include "quant.h"
 
@@ -177,6 +178,75 @@ int check_decode(const akv_decode_args *a) {
     return AKV_OK;
 }
 
+struct PrefillPlan {
+    int R, n_row_tiles, nsplit, nchunk, prows;
+    int64_t tiles_per_split, part_bytes;
+};
+
+int check_prefill(const akv_prefill_args *a) {
+    if (!a) return fail(AKV_E_INVALID, "args is NULL");
+    if (a->abi_version != AKV_ABI_VERSION)
+        return fail(AKV_E_ABI, "args built for ABI %d, library is ABI %d", a->abi_version, AKV_ABI_VERSION);
+    if (a->q_dtype != AKV_DT_F16 && a->q_dtype != AKV_DT_BF16)
+        return fail(AKV_E_DTYPE, "prefill takes float16 or bfloat16 queries");
+    if (a->D != 128) return fail(AKV_E_SHAPE, "prefill supports head_dim 128 (got %d)", a->D);
+    if (a->B < 1 || a->Hq < 1 || a->Hkv < 1 || a->M < 1) return fail(AKV_E_SHAPE, "B, Hq, Hkv, M must be >= 1");
+    if (a->Hq % a->Hkv) return fail(AKV_E_SHAPE, "Hq (%d) must be a multiple of Hkv (%d)", a->Hq, a->Hkv);
+    if (a->n_hot < 0) return fail(AKV_E_SHAPE, "n_hot < 0");
+    const akv_warm_desc &w = a->warm;
+    const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
+    if (nw < 0) return fail(AKV_E_SHAPE, "n_warm < 0");
+    if (a->n_hot + nw < 1) return fail(AKV_E_SHAPE, "no tokens to attend to");
+    if (!a->q || !a->out) return fail(AKV_E_INVALID, "q and out are required");
+    if (!aligned16(a->q) || !aligned16(a->out)) return fail(AKV_E_ALIGN, "q/out must be 16-byte aligned");
+    if (a->n_hot > 0) {
+        if (!a->k_hot || !a->v_hot) return fail(AKV_E_INVALID, "k_hot/v_hot required when n_hot > 0");
+        if (!aligned16(a->k_hot) || !aligned16(a->v_hot)) return fail(AKV_E_ALIGN, "hot tier must be 16-byte aligned");
+        if (a->n_hot * a->D * 2 >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "hot tier per head exceeds 4 GiB");
+    }
+    if (w.kind == AKV_WARM_AFFINE) {
+        for (int bits : {w.bits_k, w.bits_v})
+            if (bits < 2 || bits > 4) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
+        if (w.block_t < 32 || w.block_t % 32) return fail(AKV_E_UNSUPPORTED, "prefill needs block_t a multiple of 32");
+        if (w.group_v != 32 && w.group_v != 64 && w.group_v != 128)
+            return fail(AKV_E_UNSUPPORTED, "prefill needs group_v 32, 64 or 128");
+        if (w.n_out != 0) return fail(AKV_E_UNSUPPORTED, "prefill does not take outlier channels");
+        if (nw > 0) {
+            if (!w.k_codes || !w.v_codes || !w.k_scale || !w.k_zero || !w.v_scale || !w.v_zero)
+                return fail(AKV_E_INVALID, "warm tier pointers missing");
+            if (!aligned16(w.k_codes) || !aligned16(w.v_codes) || !aligned16(w.k_scale) || !aligned16(w.v_scale) ||
+                !aligned16(w.k_zero) || !aligned16(w.v_zero))
+                return fail(AKV_E_ALIGN, "warm tier must be 16-byte aligned");
+        }
+        if (nw * (int64_t)a->D >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "warm tier per head exceeds 4 GiB");
+    } else if (w.kind != AKV_WARM_NONE) {
+        return fail(AKV_E_UNSUPPORTED, "prefill takes the block-affine warm tier only");
+    }
+    return AKV_OK;
+}
+
+// Row tiles of 128 query rows per (batch, kv-head); token splits until there
+// are two workgroups per compute unit (two waves per SIMD hide the MFMA and
+// LDS latencies of each other), each split at least 8 tiles.
+void make_prefill_plan(const akv_prefill_args *a, PrefillPlan *pl) {
+    const int g = a->Hq / a->Hkv;
+    pl->R = g * a->M;
+    pl->n_row_tiles = (pl->R + akv::kPrefillRows - 1) / akv::kPrefillRows;
+    const int64_t nw = a->warm.kind == AKV_WARM_NONE ? 0 : a->warm.n_warm;
+    const int64_t nt = (a->n_hot + 31) / 32 + (nw + 31) / 32;
+    const int64_t wgs = (int64_t)a->B * a->Hkv * pl->n_row_tiles;
+    int64_t ns = a->num_splits > 0 ? a->num_splits : (2 * kCUs + wgs - 1) / wgs;
+    if (a->num_splits <= 0 && ns > nt / 8) ns = nt / 8;
+    if (ns > nt) ns = nt;
+    if (ns < 1) ns = 1;
+    pl->tiles_per_split = (nt + ns - 1) / ns;
+    pl->nsplit = (int)((nt + pl->tiles_per_split - 1) / pl->tiles_per_split);
+    pl->nchunk = (pl->R + 15) / 16;
+    pl->prows = pl->R < 16 ? pl->R : 16;
+    pl->part_bytes = pl->nsplit > 1
+        ? align256((int64_t)a->B * a->Hkv * pl->nchunk * pl->nsplit * pl->prows * (a->D + 4) * 4) : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -191,6 +261,7 @@ int64_t akv_struct_size(int32_t which) {
         case 2: return (int64_t)sizeof(akv_quant_args);
         case 3: return (int64_t)sizeof(akv_dequant_args);
         case 4: return (int64_t)sizeof(akv_importance_args);
+        case 5: return (int64_t)sizeof(akv_prefill_args);
         default: return -1;
     }
 }
@@ -416,6 +487,50 @@ int akv_bitunpack(const void *packed, void *codes, int64_t rows, int32_t packed_
     if ((rows > 0 && orig_dim > 0) && (!codes || !packed)) return fail(AKV_E_INVALID, "null pointer");
     hipError_t e = akv::bitunpack_launch(packed, codes, rows, packed_dim, orig_dim, bits, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "bitunpack launch");
+    return ok();
+}
+
+int64_t akv_prefill_workspace_bytes(const akv_prefill_args *a) {
+    if (check_prefill(a) != AKV_OK) return -1;
+    PrefillPlan pl;
+    make_prefill_plan(a, &pl);
+    return pl.part_bytes;
+}
+
+int akv_prefill_attn(const akv_prefill_args *a, void *stream) {
+    int rc = check_prefill(a);
+    if (rc != AKV_OK) return rc;
+    PrefillPlan pl;
+    make_prefill_plan(a, &pl);
+    if (pl.part_bytes > 0) {
+        if (!a->workspace || a->workspace_bytes < pl.part_bytes)
+            return fail(AKV_E_WORKSPACE, "workspace of %lld bytes needed", (long long)pl.part_bytes);
+        if (!aligned16(a->workspace)) return fail(AKV_E_ALIGN, "workspace must be 16-byte aligned");
+    }
+    const akv_warm_desc &w = a->warm;
+    akv::PrefillParams p{};
+    p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.M = a->M; p.g = a->Hq / a->Hkv; p.R = pl.R;
+    p.q_bf16 = a->q_dtype == AKV_DT_BF16;
+    p.q = a->q; p.out = a->out;
+    p.khot = (const _Float16 *)a->k_hot; p.vhot = (const _Float16 *)a->v_hot; p.n_hot = a->n_hot;
+    if (w.kind == AKV_WARM_AFFINE) {
+        p.kc = w.k_codes; p.vc = w.v_codes;
+        p.ks = (const _Float16 *)w.k_scale; p.kz = (const _Float16 *)w.k_zero;
+        p.vs = (const _Float16 *)w.v_scale; p.vz = (const _Float16 *)w.v_zero;
+        p.n_warm = w.n_warm; p.T = w.block_t; p.Gv = w.group_v;
+        p.nblk = (w.n_warm + w.block_t - 1) / w.block_t;
+        p.bits_k = w.bits_k; p.bits_v = w.bits_v;
+    } else {
+        p.n_warm = 0; p.T = 32; p.Gv = 32; p.nblk = 0; p.bits_k = p.bits_v = 4;
+    }
+    p.scale_log2 = a->sm_scale * 1.4426950408889634f;
+    p.n_row_tiles = pl.n_row_tiles;
+    p.nsplit = pl.nsplit;
+    p.tiles_per_split = pl.tiles_per_split;
+    p.part = (float *)a->workspace;
+    p.nchunk = pl.nchunk; p.prows = pl.prows;
+    hipError_t e = akv::prefill_launch(p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return ok();
 }
 

@@ -40,6 +40,7 @@ struct DecodeParams {
     float *stash;                 // [B][Hq][M][N] log2-domain logits (or null)
     float *rowstats;              // [B*Hq*M][2] (M, L)
     _Float16 *out;                // [B][Hq][M][D]
+    int out_bf16;                 // reduce only: write bf16 (chunked prefill with bf16 queries)
     float *attn_out;              // normalised weights (or null)
     float *scores;                // importance EMA (or null)
     int64_t n_scores;
@@ -54,6 +55,9 @@ struct DecodeParams {
 hipError_t legacy_sym_launch(const void *kz, const void *vz, int64_t n, int dt, int *flags, hipStream_t s);
 
 hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const int *sym_src, hipStream_t s);
+
+// Merge split partials (m, l, acc) into the output (and row statistics).
+hipError_t decode_reduce_launch(const DecodeParams &p, hipStream_t s);
 
 // LDS-streamed split kernel for the block-affine tier (decode_fast.hip).
 bool decode_fast_eligible(const DecodeParams &p, int wk);

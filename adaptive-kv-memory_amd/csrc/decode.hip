@@ -772,8 +772,14 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p
         const int r = row0 + rr;
         const int h = kvh * p.g + r / p.M, m = r % p.M;
         const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
-        const h4 ov = {(_Float16)(o[0] / L), (_Float16)(o[1] / L), (_Float16)(o[2] / L), (_Float16)(o[3] / L)};
-        *(h4 *)(p.out + row * D + 4 * tid) = ov;
+        if (p.out_bf16) {
+            const u2 ov = {(uint32_t)f32_to_bf16_rne(o[0] / L) | ((uint32_t)f32_to_bf16_rne(o[1] / L) << 16),
+                           (uint32_t)f32_to_bf16_rne(o[2] / L) | ((uint32_t)f32_to_bf16_rne(o[3] / L) << 16)};
+            *(u2 *)(p.out + row * D + 4 * tid) = ov;
+        } else {
+            const h4 ov = {(_Float16)(o[0] / L), (_Float16)(o[1] / L), (_Float16)(o[2] / L), (_Float16)(o[3] / L)};
+            *(h4 *)(p.out + row * D + 4 * tid) = ov;
+        }
         if (tid == 0 && p.rowstats) {
             p.rowstats[2 * row] = M;
             p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
@@ -880,6 +886,13 @@ hipError_t legacy_sym_launch(const void *kz, const void *vz, int64_t n, int dt, 
     return hipGetLastError();
 }
 
+hipError_t decode_reduce_launch(const DecodeParams &p, hipStream_t s) {
+    const dim3 rgrid(p.B * p.Hkv * p.nchunk, p.prows);
+    if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
 hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const int *sym_src_dt_n, hipStream_t s) {
     hipError_t e;
     if (wk == AKV_WARM_LEGACY && p.sym_flags && sym_src_dt_n) {
@@ -889,10 +902,7 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
     if (decode_fast_eligible(p, wk)) e = decode_fast_split_launch(p, kb, vb, s);
     else e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
-    const dim3 rgrid(p.B * p.Hkv * p.nchunk, p.prows);
-    if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(256), 0, s, p);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    if ((e = decode_reduce_launch(p, s)) != hipSuccess) return e;
     if (p.stash) {
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
         hipLaunchKernelGGL(weights_importance_kernel, dim3((unsigned)((nmax + 63) / 64)), dim3(256), 0, s, p);

@@ -1,0 +1,454 @@
+// Chunked-prefill attention over a hot fp16 + block-affine warm KV cache:
+// M query positions per head (a prompt chunk placed after every cached token,
+// so no mask over the cache) against Nh + Nw cached tokens.  MFMA-bound.
+//
+// Workgroup: 4 waves, 128 query rows of one (batch, kv-head) -- row r is
+// query head kvh*g + r / M at position r % M, so the g heads of a GQA group
+// share every dequantized tile.  Wave w owns rows 32w .. 32w+31 as two
+// 16-row MFMA column groups.
+//
+// The cache is walked in 32-token tiles (hot tiles, then warm units), double
+// buffered in LDS.  While the MFMAs consume tile j, waves 0-1 dequantize tile
+// j+1's K and waves 2-3 its V from registers loaded one tile ahead:
+//   K tile  [32 tokens][4 channel groups][16 code pairs] u32, pair order of
+//           kpair_chan() (the query operand is permuted to match), exact
+//           fp16 dequant round16(round16(c*s) + z) as in the decode kernel;
+//   V tile  the PV MFMA operand as each lane reads it: [half][channel kk of
+//           the chunk][lane] u2, values round16(c*s); the zero-points enter
+//           through one more MFMA per half with the tile's zeros
+//           [half][lane] u2 (sum_t P z, added to every channel of the group).
+// Per 16-token half and column group: S^T = K . Q^T (4 x 16x16x32), online
+// softmax in the log2 domain (P in fp16 x 2^7), O^T += V^T . P^T
+// (8 x 16x16x16 + 1 for the zero-points).
+//
+// Grid: one workgroup per (batch, kv-head, token split, row tile), the
+// (batch, kv-head) index varying fastest so that consecutive workgroups --
+// placed round-robin on the XCDs -- keep one kv-head's tiles in one L2.
+// With one split the output is written directly; with more, the partials
+// (m, l, acc) go to the decode split layout and decode_reduce_kernel merges.
+#include "akv_common.h"
+#include "decode.h"
+#include "prefill.h"
+#include "tile_common.h"
+
+namespace akv {
+
+namespace {
+
+constexpr int kPD = 128;
+constexpr int kPTok = 32;                      // tokens per tile
+constexpr int kPThreads = 256;
+constexpr int kKRow = 256 + 16;                // K tile row bytes (padded against bank conflicts)
+constexpr int kKTile = kPTok * kKRow;          // 8704
+constexpr int kVTile = 2 * 8 * 64 * 8;         // 8192
+constexpr int kVzTile = 2 * 64 * 8;            // 1024
+constexpr int kBuf = kKTile + kVTile + kVzTile;
+constexpr int kPKmeta = 3 * 4 * 16 * 4;        // [s | n | z][group][pair] u32, per K wave
+constexpr int kPLds = 2 * kBuf + 2 * kPKmeta;
+
+// bf16 pair (one dword) -> fp16 pair (exact for values in fp16's normal range)
+__device__ __forceinline__ uint32_t bf16x2_to_h2(uint32_t w) {
+    const h2 v = {(_Float16)bf16_to_f32((uint16_t)w), (_Float16)bf16_to_f32((uint16_t)(w >> 16))};
+    return as_u32(v);
+}
+
+}  // namespace
+
+template <int BK, int BV, int NG>
+__global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams p) {
+    constexpr int KR = 16 * BK, VR = 16 * BV, GV = kPD / NG;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int col = lane & 15, grp = lane >> 4;
+
+    // ---- workgroup -> (batch, kv-head, split, row tile); (b, kv-head) fastest
+    const int npair = p.B * p.Hkv;
+    const int id = blockIdx.x;
+    const int pair = id % npair;
+    const int rest = id / npair;
+    const int split = rest % p.nsplit;
+    const int rtile = rest / p.nsplit;
+    const int b = pair / p.Hkv, kvh = pair % p.Hkv;
+    const int64_t bh = (int64_t)b * p.Hkv + kvh;
+    const int r0 = rtile * kPrefillRows;
+
+    // ---- token tiles of this split: hot tiles first, then warm units
+    const int64_t n_ht = (p.n_hot + kPTok - 1) / kPTok, n_wt = (p.n_warm + kPTok - 1) / kPTok;
+    const int64_t nt = n_ht + n_wt;
+    const int64_t t_begin = min((int64_t)split * p.tiles_per_split, nt);
+    const int64_t t_end = min(t_begin + p.tiles_per_split, nt);
+
+    // ---- query operand of the wave's two column groups (rows past R repeat row r0)
+    const float sl2 = p.scale_log2;
+    h8 qop[2][4];
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+        const int r = r0 + 32 * wave + 16 * rg + col;
+        const int rc = r < p.R ? r : r0;
+        const int hq = kvh * p.g + rc / p.M, mq = rc % p.M;
+        const int64_t qoff = ((int64_t)(b * p.Hq + hq) * p.M + mq) * kPD + 32 * grp;
+        const u4 *src = (const u4 *)((const uint16_t *)p.q + qoff);
+        uint32_t nat[16], pairs[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const u4 x = src[q4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t xe = x[e];
+                nat[4 * q4 + e] = p.q_bf16 ? bf16x2_to_h2(xe) : xe;
+            }
+        }
+        hot_k_pairs<BK>(nat, pairs);
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+            qop[rg][st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
+    }
+
+    Soft sm[2];
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+        sm[rg].m2 = -INFINITY;
+        sm[rg].l = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sm[rg].acc[j] = (f4){0.f, 0.f, 0.f, 0.f};
+        sm[rg].accz = (f4){0.f, 0.f, 0.f, 0.f};
+    }
+
+    // ---- staging roles
+    // K (waves 0, 1): token 16*wave + col of the tile, channel group grp;
+    //   meta prep: channel pair pi2 of group g2 (as in the decode kernel).
+    // V (waves 2, 3): half h = wave - 2, chunk col (8 channels), tokens 16h + 4grp + i.
+    const bool kwave = wave < 2;
+    const int ktok = 16 * (wave & 1) + col;
+    const int g2 = lane >> 4, pi2 = lane & 15;
+    const int kch_lo = 32 * g2 + kpair_chan<BK>(pi2, 0), kch_hi = 32 * g2 + kpair_chan<BK>(pi2, 1);
+    const _Float16 nmul = (_Float16)(-magic_val(koff<BK>(pi2)));
+    const int vh = wave & 1;
+    const int gv = (8 * col) / GV;
+    unsigned char *kmeta = smem + 2 * kBuf + (wave & 1) * kPKmeta;
+
+    const __amdgpu_buffer_rsrc_t rkc = make_rsrc((const unsigned char *)p.kc + bh * p.n_warm * KR, (uint32_t)(p.n_warm * KR));
+    const __amdgpu_buffer_rsrc_t rvc = make_rsrc((const unsigned char *)p.vc + bh * p.n_warm * VR, (uint32_t)(p.n_warm * VR));
+    const __amdgpu_buffer_rsrc_t rks = make_rsrc(p.ks + bh * p.nblk * kPD, (uint32_t)(p.nblk * kPD * 2));
+    const __amdgpu_buffer_rsrc_t rkz = make_rsrc(p.kz + bh * p.nblk * kPD, (uint32_t)(p.nblk * kPD * 2));
+    const __amdgpu_buffer_rsrc_t rvs = make_rsrc(p.vs + bh * p.n_warm * NG, (uint32_t)(p.n_warm * NG * 2));
+    const __amdgpu_buffer_rsrc_t rvz = make_rsrc(p.vz + bh * p.n_warm * NG, (uint32_t)(p.n_warm * NG * 2));
+    const __amdgpu_buffer_rsrc_t rkh = make_rsrc(p.khot + bh * p.n_hot * kPD, (uint32_t)(p.n_hot * kPD * 2));
+    const __amdgpu_buffer_rsrc_t rvh = make_rsrc(p.vhot + bh * p.n_hot * kPD, (uint32_t)(p.n_hot * kPD * 2));
+
+    Masks<BK> km;
+    km.init();
+    Masks<BV> vmk;
+    vmk.init();
+
+    // registers of the next tile
+    uint32_t kraw[4] = {0u, 0u, 0u, 0u};
+    uint32_t kmr[4] = {0u, 0u, 0u, 0u};  // s_lo, s_hi, z_lo, z_hi of the prep pair
+    uint32_t vraw[4] = {0u, 0u, 0u, 0u};
+    uint32_t vsr[4] = {0u, 0u, 0u, 0u}, vzr[4] = {0u, 0u, 0u, 0u};
+    u4 hraw[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) hraw[i] = (u4){0u, 0u, 0u, 0u};
+
+    // Global loads of tile t into the lane's registers (ranges past the end read 0).
+    auto load_tile = [&](int64_t t) {
+        if (t < n_ht) {
+            const int64_t tok0 = t * kPTok;
+            if (kwave) {
+                const uint32_t off = (uint32_t)((tok0 + ktok) * kPD + 32 * grp) * 2u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hraw[i] = bld128(rkh, off + 16u * i);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t off = (uint32_t)((tok0 + 16 * vh + 4 * grp + i) * kPD + 8 * col) * 2u;
+                    hraw[i] = bld128(rvh, off);
+                }
+            }
+        } else {
+            const int64_t u = t - n_ht, tok0 = u * kPTok;
+            if (kwave) {
+                const uint32_t off = (uint32_t)((tok0 + ktok) * KR + grp * 4 * BK);
+#pragma unroll
+                for (int i = 0; i < BK; ++i) kraw[i] = bld32(rkc, off + 4u * i);
+                const uint32_t mrow = (uint32_t)(tok0 / p.T) * kPD;
+                kmr[0] = bld16(rks, (mrow + kch_lo) * 2u);
+                kmr[1] = bld16(rks, (mrow + kch_hi) * 2u);
+                kmr[2] = bld16(rkz, (mrow + kch_lo) * 2u);
+                kmr[3] = bld16(rkz, (mrow + kch_hi) * 2u);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t tk = (uint32_t)(tok0 + 16 * vh + 4 * grp + i);
+                    if (BV == 3) {
+                        const uint32_t off = tk * VR + 3 * col;
+                        const uint32_t d0 = bld32(rvc, off & ~3u);
+                        const uint32_t d1 = (off & 3u) >= 2u ? bld32(rvc, (off & ~3u) + 4u) : 0u;
+                        vraw[i] = __builtin_amdgcn_alignbyte(d1, d0, off & 3u);
+                    } else if (BV == 4) {
+                        vraw[i] = bld32(rvc, tk * VR + 4 * col);
+                    } else {
+                        vraw[i] = bld16(rvc, tk * VR + 2 * col);
+                    }
+                    vsr[i] = bld16(rvs, (tk * NG + gv) * 2u);
+                    vzr[i] = bld16(rvz, (tk * NG + gv) * 2u);
+                }
+            }
+        }
+    };
+
+    // Dequantize the registers of tile t into LDS buffer `buf`.
+    auto stage_tile = [&](int64_t t, unsigned char *buf) {
+        unsigned char *kt = buf, *vt = buf + kKTile, *vzt = buf + kKTile + kVTile;
+        if (t < n_ht) {
+            if (kwave) {
+                uint32_t nat[16], pairs[16];
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t xe = hraw[q4][e];
+                        nat[4 * q4 + e] = xe;
+                    }
+                hot_k_pairs<BK>(nat, pairs);
+                u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64);
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+                    dst[q4] = (u4){pairs[4 * q4], pairs[4 * q4 + 1], pairs[4 * q4 + 2], pairs[4 * q4 + 3]};
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                    const uint32_t sel = (kk & 1) ? 0x07060302u : 0x05040100u;
+                    const uint32_t lo = perm(hraw[1][kk / 2], hraw[0][kk / 2], sel);
+                    const uint32_t hi = perm(hraw[3][kk / 2], hraw[2][kk / 2], sel);
+                    *(u2 *)(vt + ((vh * 8 + kk) * 64 + lane) * 8) = (u2){lo, hi};
+                }
+            }
+            return;
+        }
+        if (kwave) {
+            // K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared through LDS
+            const h2 s2v = as_h2(kmr[0] | (kmr[1] << 16));
+            const h2 z2v = as_h2(kmr[2] | (kmr[3] << 16));
+            const h2 n2 = s2v * (h2){nmul, nmul};
+            const bool kfast = !__builtin_amdgcn_ballot_w64(!finite2(as_u32(n2)));
+            uint32_t *kmw = (uint32_t *)kmeta;
+            kmw[(0 * 4 + g2) * 16 + pi2] = as_u32(s2v);
+            kmw[(1 * 4 + g2) * 16 + pi2] = as_u32(n2);
+            kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
+            __builtin_amdgcn_wave_barrier();
+            h2 ksc[16], kng[16], kze[16];
+            const u4 *srcm = (const u4 *)kmeta;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const u4 av = srcm[(0 * 4 + grp) * 4 + q4];
+                const u4 nv = srcm[(1 * 4 + grp) * 4 + q4];
+                const u4 zv = srcm[(2 * 4 + grp) * 4 + q4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t ae = av[e], ne = nv[e], ze = zv[e];
+                    ksc[4 * q4 + e] = as_h2(ae);
+                    kng[4 * q4 + e] = as_h2(ne);
+                    kze[4 * q4 + e] = as_h2(ze);
+                }
+            }
+            KWin<BK> W;
+            k_windows<BK>(kraw, W);
+            uint32_t out[16];
+#pragma unroll
+            for (int pi = 0; pi < 16; ++pi) {
+                const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                h2 v;
+                if (kfast) {
+                    v = pk_fma(as_h2(uu), ksc[pi], kng[pi]);
+                } else {
+                    const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
+                    v = (as_h2(uu) - (h2){mv, mv}) * ksc[pi];
+                }
+                v = v + kze[pi];
+                out[pi] = as_u32(v);
+            }
+            u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64);
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) dst[q4] = (u4){out[4 * q4], out[4 * q4 + 1], out[4 * q4 + 2], out[4 * q4 + 3]};
+            __builtin_amdgcn_wave_barrier();  // kmeta reads done before the next tile's writes
+        } else {
+            h2 vs[2], vz[2];
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                vs[pp] = as_h2(vsr[2 * pp] | (vsr[2 * pp + 1] << 16));
+                vz[pp] = as_h2(vzr[2 * pp] | (vzr[2 * pp + 1] << 16));
+            }
+            bool vfin = true;
+            {
+                const _Float16 n0 = (_Float16)(-1024.0f);
+                vfin = finite2(as_u32(vs[0] * (h2){n0, n0})) && finite2(as_u32(vs[1] * (h2){n0, n0}));
+            }
+            const bool vfast = !__builtin_amdgcn_ballot_w64(!vfin);
+            uint32_t vpair[2][8];
+#pragma unroll
+            for (int pp = 0; pp < 2; ++pp) {
+                uint32_t win[VSlot<BV>::NW];
+                v_windows<BV>(vraw[2 * pp], vraw[2 * pp + 1], win);
+                if (vfast) {
+                    h2 vn[v_noffs<BV>()];
+#pragma unroll
+                    for (int oi = 0; oi < v_noffs<BV>(); ++oi) {
+                        const _Float16 m = (_Float16)(-magic_val(oi * v_ostep<BV>()));
+                        vn[oi] = vs[pp] * (h2){m, m};
+                    }
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) {
+                        const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                        vpair[pp][kk] = as_u32(pk_fma(as_h2(uu), vs[pp], vn[voff<BV>(kk) / v_ostep<BV>()]));
+                    }
+                } else {
+#pragma unroll
+                    for (int kk = 0; kk < 8; ++kk) {
+                        const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                        const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
+                        vpair[pp][kk] = as_u32((as_h2(uu) - (h2){mv, mv}) * vs[pp]);
+                    }
+                }
+            }
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) *(u2 *)(vt + ((vh * 8 + kk) * 64 + lane) * 8) = (u2){vpair[0][kk], vpair[1][kk]};
+            *(u2 *)(vzt + (vh * 64 + lane) * 8) = (u2){as_u32(vz[0]), as_u32(vz[1])};
+        }
+    };
+
+    // ---- the tile loop: load t+1 | MFMA on t | dequant t+1 | barrier
+    if (t_begin < t_end) {
+        load_tile(t_begin);
+        stage_tile(t_begin, smem);
+    }
+    __syncthreads();
+    for (int64_t t = t_begin; t < t_end; ++t) {
+        const int cur = (int)((t - t_begin) & 1);
+        unsigned char *buf = smem + cur * kBuf;
+        const bool more = t + 1 < t_end;
+        if (more) load_tile(t + 1);
+
+        const bool hot = t < n_ht;
+        const int64_t tok0 = (hot ? t : t - n_ht) * kPTok;
+        const int64_t ntok = hot ? p.n_hot : p.n_warm;
+        const unsigned char *kt = buf, *vt = buf + kKTile, *vzt = buf + kKTile + kVTile;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            f4 sc[2] = {(f4){0.f, 0.f, 0.f, 0.f}, (f4){0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const h8 a = *(const h8 *)(kt + (16 * h + col) * kKRow + grp * 64 + 16 * st);
+                sc[0] = mfma_k32(a, qop[0][st], sc[0]);
+                sc[1] = mfma_k32(a, qop[1][st], sc[1]);
+            }
+            const int64_t first = tok0 + 16 * h + 4 * grp;  // token of sc[.][0]
+            if (tok0 + 16 * h + 16 > ntok) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (first + i >= ntok) {
+                        sc[0][i] = -INFINITY;
+                        sc[1][i] = -INFINITY;
+                    }
+            }
+            h4 pop[2];
+            pop[0] = softmax16(sm[0], sc[0], sl2);
+            pop[1] = softmax16(sm[1], sc[1], sl2);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const h4 a = *(const h4 *)(vt + ((h * 8 + kk) * 64 + lane) * 8);
+                sm[0].acc[kk] = mfma_k16(a, pop[0], sm[0].acc[kk]);
+                sm[1].acc[kk] = mfma_k16(a, pop[1], sm[1].acc[kk]);
+            }
+            if (!hot) {
+                const h4 az = *(const h4 *)(vzt + (h * 64 + lane) * 8);
+                sm[0].accz = mfma_k16(az, pop[0], sm[0].accz);
+                sm[1].accz = mfma_k16(az, pop[1], sm[1].accz);
+            }
+        }
+
+        if (more) stage_tile(t + 1, smem + (cur ^ 1) * kBuf);
+        __syncthreads();
+    }
+
+    // ---- output (one split) or partials (decode split layout)
+#pragma unroll
+    for (int rg = 0; rg < 2; ++rg) {
+        const float l = wsum16(sm[rg].l);
+        const int r = r0 + 32 * wave + 16 * rg + col;
+        if (r >= p.R) continue;
+        if (p.nsplit == 1) {
+            const int hq = kvh * p.g + r / p.M, mq = r % p.M;
+            const int64_t orow = ((int64_t)(b * p.Hq + hq) * p.M + mq) * kPD;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float o[8];
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) o[kk] = (sm[rg].acc[kk][i] + sm[rg].accz[i]) / l;
+                uint32_t w[4];
+                if (p.q_bf16) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        w[e] = (uint32_t)f32_to_bf16_rne(o[2 * e]) | ((uint32_t)f32_to_bf16_rne(o[2 * e + 1]) << 16);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w[e] = as_u32((h2){(_Float16)o[2 * e], (_Float16)o[2 * e + 1]});
+                }
+                *(u4 *)((uint16_t *)p.out + orow + 8 * (4 * grp + i)) = (u4){w[0], w[1], w[2], w[3]};
+            }
+        } else {
+            const int chunk = r / 16, rr = r % 16;
+            float *part = p.part + ((bh * p.nchunk + chunk) * p.nsplit + split) * (int64_t)(p.prows * (kPD + 4)) +
+                          rr * (kPD + 4);
+            if (grp == 0) {
+                part[0] = sm[rg].m2;
+                part[1] = l;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                f4 *dst = (f4 *)(part + 4 + 8 * (4 * grp + i));
+                dst[0] = (f4){sm[rg].acc[0][i] + sm[rg].accz[i], sm[rg].acc[1][i] + sm[rg].accz[i],
+                              sm[rg].acc[2][i] + sm[rg].accz[i], sm[rg].acc[3][i] + sm[rg].accz[i]};
+                dst[1] = (f4){sm[rg].acc[4][i] + sm[rg].accz[i], sm[rg].acc[5][i] + sm[rg].accz[i],
+                              sm[rg].acc[6][i] + sm[rg].accz[i], sm[rg].acc[7][i] + sm[rg].accz[i]};
+            }
+        }
+    }
+}
+
+int prefill_lds_bytes() { return kPLds; }
+
+template <int BK, int BV, int NG>
+static hipError_t launch_prefill(const PrefillParams &p, hipStream_t s) {
+    const unsigned nwg = (unsigned)(p.B * p.Hkv * p.nsplit * p.n_row_tiles);
+    hipLaunchKernelGGL((prefill_kernel<BK, BV, NG>), dim3(nwg), dim3(kPThreads), kPLds, s, p);
+    return hipGetLastError();
+}
+
+template <int BK, int BV>
+static hipError_t launch_prefill_ng(const PrefillParams &p, hipStream_t s) {
+    if (p.Gv == 32) return launch_prefill<BK, BV, 4>(p, s);
+    if (p.Gv == 64) return launch_prefill<BK, BV, 2>(p, s);
+    if (p.Gv == 128) return launch_prefill<BK, BV, 1>(p, s);
+    return hipErrorInvalidValue;
+}
+
+hipError_t prefill_launch(const PrefillParams &p, hipStream_t s) {
+    hipError_t e = hipErrorInvalidValue;
+#define AKV_PKV(a, c) \
+    if (p.bits_k == a && p.bits_v == c) e = launch_prefill_ng<a, c>(p, s);
+    AKV_PKV(2, 2) AKV_PKV(2, 3) AKV_PKV(2, 4) AKV_PKV(3, 2) AKV_PKV(3, 3) AKV_PKV(3, 4) AKV_PKV(4, 2) AKV_PKV(4, 3)
+    AKV_PKV(4, 4)
+#undef AKV_PKV
+    if (e != hipSuccess || p.nsplit == 1) return e;
+    DecodeParams d{};
+    d.B = p.B; d.Hq = p.Hq; d.Hkv = p.Hkv; d.M = p.M; d.D = kPD; d.g = p.g; d.R = p.R;
+    d.nchunk = p.nchunk; d.prows = p.prows; d.nsplit = p.nsplit;
+    d.part = p.part;
+    d.out = (_Float16 *)p.out;
+    d.out_bf16 = p.q_bf16;
+    return decode_reduce_launch(d, s);
+}
+
+}  // namespace akv

@@ -215,13 +215,43 @@ typedef struct akv_importance_args {
  * ImportanceScorer.update's accumulate rule (akv/importance.py:88-92, :127-128). */
 int akv_importance_update(const akv_importance_args *args, void *stream);
 
+/* --------------------------------------------------------------- prefill */
+
+typedef struct akv_prefill_args {
+    int32_t abi_version;   /* AKV_ABI_VERSION */
+    int32_t B, Hq, Hkv, M, D;  /* D = 128; Hq % Hkv == 0; M query positions per head */
+    int32_t q_dtype;       /* AKV_DT_F16 or AKV_DT_BF16 (bf16 is converted to fp16: exact in fp16's range) */
+    const void *q;         /* [B][Hq][M][D] */
+    const void *k_hot, *v_hot; /* [B][Hkv][n_hot][D] f16 (may be NULL when n_hot == 0) */
+    int64_t n_hot;
+    float sm_scale;        /* softmax scale (1/sqrt(D) in the reference) */
+    int32_t num_splits;    /* token splits, 0 = choose */
+    akv_warm_desc warm;    /* AKV_WARM_NONE, or AKV_WARM_AFFINE with block_t % 32 == 0,
+                              group_v in {32, 64, 128} and n_out == 0 */
+    void *out;             /* [B][Hq][M][D], q dtype */
+    void *workspace;       /* akv_prefill_workspace_bytes() bytes (0 with a single split) */
+    int64_t workspace_bytes;
+} akv_prefill_args;
+
+/* Bytes of device workspace akv_prefill_attn needs for `args` (split partials). */
+int64_t akv_prefill_workspace_bytes(const akv_prefill_args *args);
+
+/* Chunked prefill: M query positions per head (a prompt chunk after every
+ * cached token, so no mask over the cache) attend to the hot fp16 + warm
+ * block-affine cache; no attention weights.  QK^T and PV run on MFMA over
+ * dequantized LDS tiles shared by the GQA group's heads.
+ * Replaces, for M > 1 without weights: triton_ops.fused_quantized_attention
+ * (akv/triton_ops.py:330-377) and triton_ops.fused_mixed_precision_attention
+ * (akv/triton_ops.py:466-515), which dequantize the whole warm tier first. */
+int akv_prefill_attn(const akv_prefill_args *args, void *stream);
+
 /* --------------------------------------------------------------- misc */
 
 int akv_abi_version(void);
 const char *akv_last_error(void);
 /* sizeof of the args structs, for bindings that mirror them (ctypes, cgo):
  * 0 akv_warm_desc, 1 akv_decode_args, 2 akv_quant_args, 3 akv_dequant_args,
- * 4 akv_importance_args; -1 for an unknown id. */
+ * 4 akv_importance_args, 5 akv_prefill_args; -1 for an unknown id. */
 int64_t akv_struct_size(int32_t which);
 
 #ifdef __cplusplus

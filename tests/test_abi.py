@@ -72,3 +72,49 @@ def test_decode_shape_checks():
     a.Hkv, a.D = 2, 96
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1
     assert b"head_dim" in lib.akv_last_error()
+
+
+def _prefill_args(nat, **kw):
+    a = nat.PrefillArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.B, a.Hq, a.Hkv, a.M, a.D = 1, 64, 8, 512, 128
+    a.q_dtype = nat.DT_BF16
+    a.q = a.out = a.k_hot = a.v_hot = 0x10000  # host-side checks only: never dereferenced
+    a.n_hot = 4096
+    a.sm_scale = 128 ** -0.5
+    a.warm.kind = nat.WARM_AFFINE
+    a.warm.bits_k = a.warm.bits_v = 2
+    a.warm.n_warm = 126976
+    a.warm.block_t, a.warm.group_v = 32, 32
+    a.warm.k_codes = a.warm.v_codes = a.warm.k_scale = a.warm.k_zero = a.warm.v_scale = a.warm.v_zero = 0x20000
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_prefill_planning_and_checks():
+    from akv import _native as nat
+    lib = nat.load()
+    a = _prefill_args(nat)
+    # 128k workload: 32 row tiles x 8 kv-heads x 2 token splits = two workgroups per CU
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) == 8 * 256 * 2 * 16 * 132 * 4
+    a = _prefill_args(nat, num_splits=1)
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) == 0
+    # a short chunk splits the cache: partials of (B*Hkv*ceil(R/16)) chunks x splits x 16 rows x (D+4) fp32
+    a = _prefill_args(nat, M=16)
+    nb = lib.akv_prefill_workspace_bytes(ctypes.byref(a))
+    assert nb > 0 and nb % 256 == 0
+    assert nb >= 1 * 8 * 8 * 2 * 16 * 132 * 4
+    a = _prefill_args(nat, D=64)
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) == -1
+    assert b"head_dim 128" in lib.akv_last_error()
+    a = _prefill_args(nat, q_dtype=nat.DT_F32)
+    assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_DTYPE
+    a = _prefill_args(nat)
+    a.warm.block_t = 16
+    assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_UNSUPPORTED
+    a = _prefill_args(nat)
+    a.warm.n_out = 1
+    assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_UNSUPPORTED
+    a = _prefill_args(nat, M=16, num_splits=3)
+    assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_WORKSPACE
