@@ -13,13 +13,13 @@
 //   K tile  [32 tokens][4 channel groups][16 code pairs] u32, pair order of
 //           kpair_chan() (the query operand is permuted to match), exact
 //           fp16 dequant round16(round16(c*s) + z) as in the decode kernel;
-//   V tile  the PV MFMA operand as each lane reads it: [half][channel kk of
-//           the chunk][lane] u2, values round16(c*s); the zero-points enter
-//           through one more MFMA per half with the tile's zeros
-//           [half][lane] u2 (sum_t P z, added to every channel of the group).
-// Per 16-token half and column group: S^T = K . Q^T (4 x 16x16x32), online
-// softmax in the log2 domain (P in fp16 x 2^7), O^T += V^T . P^T
-// (8 x 16x16x16 + 1 for the zero-points).
+//   V tile  the PV MFMA operand as each lane reads it: [channel kk of the
+//           chunk][lane][half] u2, values round16(c*s); the zero-points
+//           enter through one more MFMA with the tile's zeros [lane][half]
+//           u2 (sum_t P z, added to every channel of the group).
+// Per column group: S^T = K . Q^T for each 16-token half (4 x 16x16x32),
+// online softmax over the 32 tokens in the log2 domain (P in fp16 x 2^7),
+// O^T += V^T . P^T over the 32 tokens (8 x 16x16x32 + 1 for the zeros).
 //
 // Grid: one workgroup per (batch, kv-head, token split, row tile), the
 // (batch, kv-head) index varying fastest so that consecutive workgroups --
@@ -55,7 +55,8 @@ __device__ __forceinline__ uint32_t bf16x2_to_h2(uint32_t w) {
 }  // namespace
 
 template <int BK, int BV, int NG>
-__global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams p) {
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_kernel(const PrefillParams p) {
     constexpr int KR = 16 * BK, VR = 16 * BV, GV = kPD / NG;
     extern __shared__ __align__(16) unsigned char smem[];
     const int lane = threadIdx.x & 63;
@@ -142,11 +143,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
     Masks<BV> vmk;
     vmk.init();
 
-    // registers of the next tile
-    uint32_t kraw[4] = {0u, 0u, 0u, 0u};
-    uint32_t kmr[4] = {0u, 0u, 0u, 0u};  // s_lo, s_hi, z_lo, z_hi of the prep pair
-    uint32_t vraw[4] = {0u, 0u, 0u, 0u};
-    uint32_t vsr[4] = {0u, 0u, 0u, 0u}, vzr[4] = {0u, 0u, 0u, 0u};
+    // Registers of the next tile, one set for every role:
+    //   hot K: hraw[0..3] = 64 B of the token;  hot V: hraw[i] = 16 B of token i;
+    //   warm K: hraw[0] = code bytes, hraw[1] = s_lo, s_hi, z_lo, z_hi of the prep pair;
+    //   warm V: hraw[0] = the chunk's codes of tokens 0..3, hraw[1] = scales, hraw[2] = zeros.
     u4 hraw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) hraw[i] = (u4){0u, 0u, 0u, 0u};
@@ -170,13 +170,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
             const int64_t u = t - n_ht, tok0 = u * kPTok;
             if (kwave) {
                 const uint32_t off = (uint32_t)((tok0 + ktok) * KR + grp * 4 * BK);
-#pragma unroll
-                for (int i = 0; i < BK; ++i) kraw[i] = bld32(rkc, off + 4u * i);
+                if (BK == 4) hraw[0] = bld128(rkc, off);
+                else if (BK == 3) {
+                    const u3 x = bld96(rkc, off);
+                    hraw[0] = (u4){x[0], x[1], x[2], 0u};
+                } else {
+                    const u2 x = bld64(rkc, off);
+                    hraw[0] = (u4){x[0], x[1], 0u, 0u};
+                }
                 const uint32_t mrow = (uint32_t)(tok0 / p.T) * kPD;
-                kmr[0] = bld16(rks, (mrow + kch_lo) * 2u);
-                kmr[1] = bld16(rks, (mrow + kch_hi) * 2u);
-                kmr[2] = bld16(rkz, (mrow + kch_lo) * 2u);
-                kmr[3] = bld16(rkz, (mrow + kch_hi) * 2u);
+                hraw[1] = (u4){bld16(rks, (mrow + kch_lo) * 2u), bld16(rks, (mrow + kch_hi) * 2u),
+                               bld16(rkz, (mrow + kch_lo) * 2u), bld16(rkz, (mrow + kch_hi) * 2u)};
             } else {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -185,14 +189,14 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
                         const uint32_t off = tk * VR + 3 * col;
                         const uint32_t d0 = bld32(rvc, off & ~3u);
                         const uint32_t d1 = (off & 3u) >= 2u ? bld32(rvc, (off & ~3u) + 4u) : 0u;
-                        vraw[i] = __builtin_amdgcn_alignbyte(d1, d0, off & 3u);
+                        hraw[0][i] = __builtin_amdgcn_alignbyte(d1, d0, off & 3u);
                     } else if (BV == 4) {
-                        vraw[i] = bld32(rvc, tk * VR + 4 * col);
+                        hraw[0][i] = bld32(rvc, tk * VR + 4 * col);
                     } else {
-                        vraw[i] = bld16(rvc, tk * VR + 2 * col);
+                        hraw[0][i] = bld16(rvc, tk * VR + 2 * col);
                     }
-                    vsr[i] = bld16(rvs, (tk * NG + gv) * 2u);
-                    vzr[i] = bld16(rvz, (tk * NG + gv) * 2u);
+                    hraw[1][i] = bld16(rvs, (tk * NG + gv) * 2u);
+                    hraw[2][i] = bld16(rvz, (tk * NG + gv) * 2u);
                 }
             }
         }
@@ -222,15 +226,15 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
                     const uint32_t sel = (kk & 1) ? 0x07060302u : 0x05040100u;
                     const uint32_t lo = perm(hraw[1][kk / 2], hraw[0][kk / 2], sel);
                     const uint32_t hi = perm(hraw[3][kk / 2], hraw[2][kk / 2], sel);
-                    *(u2 *)(vt + ((vh * 8 + kk) * 64 + lane) * 8) = (u2){lo, hi};
+                    *(u2 *)(vt + ((kk * 64 + lane) * 2 + vh) * 8) = (u2){lo, hi};
                 }
             }
             return;
         }
         if (kwave) {
             // K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared through LDS
-            const h2 s2v = as_h2(kmr[0] | (kmr[1] << 16));
-            const h2 z2v = as_h2(kmr[2] | (kmr[3] << 16));
+            const h2 s2v = as_h2(hraw[1][0] | (hraw[1][1] << 16));
+            const h2 z2v = as_h2(hraw[1][2] | (hraw[1][3] << 16));
             const h2 n2 = s2v * (h2){nmul, nmul};
             const bool kfast = !__builtin_amdgcn_ballot_w64(!finite2(as_u32(n2)));
             uint32_t *kmw = (uint32_t *)kmeta;
@@ -254,20 +258,22 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
                 }
             }
             KWin<BK> W;
+            const uint32_t kraw[4] = {hraw[0][0], hraw[0][1], hraw[0][2], hraw[0][3]};
             k_windows<BK>(kraw, W);
             uint32_t out[16];
+            if (kfast) {
 #pragma unroll
-            for (int pi = 0; pi < 16; ++pi) {
-                const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
-                h2 v;
-                if (kfast) {
-                    v = pk_fma(as_h2(uu), ksc[pi], kng[pi]);
-                } else {
-                    const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
-                    v = (as_h2(uu) - (h2){mv, mv}) * ksc[pi];
+                for (int pi = 0; pi < 16; ++pi) {
+                    const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                    out[pi] = as_u32(pk_fma(as_h2(uu), ksc[pi], kng[pi]) + kze[pi]);
                 }
-                v = v + kze[pi];
-                out[pi] = as_u32(v);
+            } else {
+#pragma unroll
+                for (int pi = 0; pi < 16; ++pi) {
+                    const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                    const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
+                    out[pi] = as_u32((as_h2(uu) - (h2){mv, mv}) * ksc[pi] + kze[pi]);
+                }
             }
             u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64);
 #pragma unroll
@@ -277,8 +283,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
             h2 vs[2], vz[2];
 #pragma unroll
             for (int pp = 0; pp < 2; ++pp) {
-                vs[pp] = as_h2(vsr[2 * pp] | (vsr[2 * pp + 1] << 16));
-                vz[pp] = as_h2(vzr[2 * pp] | (vzr[2 * pp + 1] << 16));
+                vs[pp] = as_h2(hraw[1][2 * pp] | (hraw[1][2 * pp + 1] << 16));
+                vz[pp] = as_h2(hraw[2][2 * pp] | (hraw[2][2 * pp + 1] << 16));
             }
             bool vfin = true;
             {
@@ -290,7 +296,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
 #pragma unroll
             for (int pp = 0; pp < 2; ++pp) {
                 uint32_t win[VSlot<BV>::NW];
-                v_windows<BV>(vraw[2 * pp], vraw[2 * pp + 1], win);
+                v_windows<BV>(hraw[0][2 * pp], hraw[0][2 * pp + 1], win);
                 if (vfast) {
                     h2 vn[v_noffs<BV>()];
 #pragma unroll
@@ -313,8 +319,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
                 }
             }
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) *(u2 *)(vt + ((vh * 8 + kk) * 64 + lane) * 8) = (u2){vpair[0][kk], vpair[1][kk]};
-            *(u2 *)(vzt + (vh * 64 + lane) * 8) = (u2){as_u32(vz[0]), as_u32(vz[1])};
+            for (int kk = 0; kk < 8; ++kk) *(u2 *)(vt + ((kk * 64 + lane) * 2 + vh) * 8) = (u2){vpair[0][kk], vpair[1][kk]};
+            *(u2 *)(vzt + (lane * 2 + vh) * 8) = (u2){as_u32(vz[0]), as_u32(vz[1])};
         }
     };
 
@@ -334,38 +340,41 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(const PrefillParams 
         const int64_t tok0 = (hot ? t : t - n_ht) * kPTok;
         const int64_t ntok = hot ? p.n_hot : p.n_warm;
         const unsigned char *kt = buf, *vt = buf + kKTile, *vzt = buf + kKTile + kVTile;
+        f4 sc[2][2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            f4 sc[2] = {(f4){0.f, 0.f, 0.f, 0.f}, (f4){0.f, 0.f, 0.f, 0.f}};
+            sc[0][h] = (f4){0.f, 0.f, 0.f, 0.f};
+            sc[1][h] = (f4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int st = 0; st < 4; ++st) {
                 const h8 a = *(const h8 *)(kt + (16 * h + col) * kKRow + grp * 64 + 16 * st);
-                sc[0] = mfma_k32(a, qop[0][st], sc[0]);
-                sc[1] = mfma_k32(a, qop[1][st], sc[1]);
+                sc[0][h] = mfma_k32(a, qop[0][st], sc[0][h]);
+                sc[1][h] = mfma_k32(a, qop[1][st], sc[1][h]);
             }
-            const int64_t first = tok0 + 16 * h + 4 * grp;  // token of sc[.][0]
-            if (tok0 + 16 * h + 16 > ntok) {
+        }
+        if (tok0 + kPTok > ntok) {  // ragged last tile: tokens past the tier score -inf
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (first + i >= ntok) {
-                        sc[0][i] = -INFINITY;
-                        sc[1][i] = -INFINITY;
+                    if (tok0 + 16 * h + 4 * grp + i >= ntok) {
+                        sc[0][h][i] = -INFINITY;
+                        sc[1][h][i] = -INFINITY;
                     }
-            }
-            h4 pop[2];
-            pop[0] = softmax16(sm[0], sc[0], sl2);
-            pop[1] = softmax16(sm[1], sc[1], sl2);
+        }
+        h8 pop[2];
+        pop[0] = softmax32(sm[0], sc[0][0], sc[0][1], sl2);
+        pop[1] = softmax32(sm[1], sc[1][0], sc[1][1], sl2);
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) {
-                const h4 a = *(const h4 *)(vt + ((h * 8 + kk) * 64 + lane) * 8);
-                sm[0].acc[kk] = mfma_k16(a, pop[0], sm[0].acc[kk]);
-                sm[1].acc[kk] = mfma_k16(a, pop[1], sm[1].acc[kk]);
-            }
-            if (!hot) {
-                const h4 az = *(const h4 *)(vzt + (h * 64 + lane) * 8);
-                sm[0].accz = mfma_k16(az, pop[0], sm[0].accz);
-                sm[1].accz = mfma_k16(az, pop[1], sm[1].accz);
-            }
+        for (int kk = 0; kk < 8; ++kk) {
+            const h8 a = *(const h8 *)(vt + (kk * 64 + lane) * 16);
+            sm[0].acc[kk] = mfma_k32(a, pop[0], sm[0].acc[kk]);
+            sm[1].acc[kk] = mfma_k32(a, pop[1], sm[1].acc[kk]);
+        }
+        if (!hot) {
+            const h8 az = *(const h8 *)(vzt + lane * 16);
+            sm[0].accz = mfma_k32(az, pop[0], sm[0].accz);
+            sm[1].accz = mfma_k32(az, pop[1], sm[1].accz);
         }
 
         if (more) stage_tile(t + 1, smem + (cur ^ 1) * kBuf);

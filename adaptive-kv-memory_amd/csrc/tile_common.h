@@ -216,6 +216,34 @@ __device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
     return (h4){(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
 }
 
+// The same over a 32-token tile given as two 16-token halves: returns the
+// fp16 P^T operand of a 16x16x32 MFMA whose K index 8*grp + j is token
+// 4*grp + j of half 0 (j < 4) or of half 1 (j >= 4).
+__device__ __forceinline__ h8 softmax32(Soft &st, f4 s0, f4 s1, float sl2) {
+    const float t = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                          fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))) * sl2;
+    if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
+        const float tm2 = wmax16(t);
+        const float mn = fmaxf(st.m2, tm2);
+        const float alpha = __builtin_amdgcn_exp2f(st.m2 - mn);
+        st.l *= alpha;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) st.acc[j] *= alpha;
+        st.accz *= alpha;
+        st.m2 = mn;
+    }
+    const float bias = kPLog2F - st.m2;
+    float p[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], sl2, bias));
+        p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], sl2, bias));
+    }
+    st.l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+    return (h8){(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3],
+                (_Float16)p[4], (_Float16)p[5], (_Float16)p[6], (_Float16)p[7]};
+}
+
 __device__ __forceinline__ uint32_t lds_u16(const unsigned char *p) { return *(const uint16_t *)p; }
 __device__ __forceinline__ h2 lds_h2(const unsigned char *a, const unsigned char *b) {
     return (h2){*(const _Float16 *)a, *(const _Float16 *)b};
