@@ -225,9 +225,9 @@ int check_prefill(const akv_prefill_args *a) {
     return AKV_OK;
 }
 
-// Row tiles of 128 query rows per (batch, kv-head); token splits until there
-// are two workgroups per compute unit (two waves per SIMD hide the MFMA and
-// LDS latencies of each other), each split at least 8 tiles.
+// Row tiles of 256 query rows per (batch, kv-head); token splits until there
+// is one workgroup (8 waves, two per SIMD) per compute unit, each split at
+// least 8 tiles.
 void make_prefill_plan(const akv_prefill_args *a, PrefillPlan *pl) {
     const int g = a->Hq / a->Hkv;
     pl->R = g * a->M;
@@ -235,7 +235,7 @@ void make_prefill_plan(const akv_prefill_args *a, PrefillPlan *pl) {
     const int64_t nw = a->warm.kind == AKV_WARM_NONE ? 0 : a->warm.n_warm;
     const int64_t nt = (a->n_hot + 31) / 32 + (nw + 31) / 32;
     const int64_t wgs = (int64_t)a->B * a->Hkv * pl->n_row_tiles;
-    int64_t ns = a->num_splits > 0 ? a->num_splits : (2 * kCUs + wgs - 1) / wgs;
+    int64_t ns = a->num_splits > 0 ? a->num_splits : (kCUs + wgs - 1) / wgs;
     if (a->num_splits <= 0 && ns > nt / 8) ns = nt / 8;
     if (ns > nt) ns = nt;
     if (ns < 1) ns = 1;

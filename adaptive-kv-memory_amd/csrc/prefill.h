@@ -25,7 +25,7 @@ struct PrefillParams {
     int nchunk, prows;              // 16-row chunks of R and rows per partial (decode layout)
 };
 
-constexpr int kPrefillRows = 128;   // query rows per workgroup
+constexpr int kPrefillRows = 256;   // query rows per workgroup
 
 // Launch the split kernel and, when nsplit > 1, the merge.
 hipError_t prefill_launch(const PrefillParams &p, hipStream_t s);

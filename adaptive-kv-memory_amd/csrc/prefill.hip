@@ -2,14 +2,14 @@
 // M query positions per head (a prompt chunk placed after every cached token,
 // so no mask over the cache) against Nh + Nw cached tokens.  MFMA-bound.
 //
-// Workgroup: 4 waves, 128 query rows of one (batch, kv-head) -- row r is
+// Workgroup: 8 waves, 256 query rows of one (batch, kv-head) -- row r is
 // query head kvh*g + r / M at position r % M, so the g heads of a GQA group
 // share every dequantized tile.  Wave w owns rows 32w .. 32w+31 as two
 // 16-row MFMA column groups.
 //
 // The cache is walked in 32-token tiles (hot tiles, then warm units), double
-// buffered in LDS.  While the MFMAs consume tile j, waves 0-1 dequantize tile
-// j+1's K and waves 2-3 its V from registers loaded one tile ahead:
+// buffered in LDS.  While the MFMAs consume tile j, waves 0-3 dequantize tile
+// j+1's K and waves 4-7 its V from registers loaded one tile ahead:
 //   K tile  [32 tokens][4 channel groups][16 code pairs] u32, pair order of
 //           kpair_chan() (the query operand is permuted to match), exact
 //           fp16 dequant round16(round16(c*s) + z) as in the decode kernel;
@@ -37,14 +37,14 @@ namespace {
 
 constexpr int kPD = 128;
 constexpr int kPTok = 32;                      // tokens per tile
-constexpr int kPThreads = 256;
+constexpr int kPThreads = 512;                 // 8 waves, 32 query rows each
 constexpr int kKRow = 256 + 16;                // K tile row bytes (padded against bank conflicts)
 constexpr int kKTile = kPTok * kKRow;          // 8704
 constexpr int kVTile = 2 * 8 * 64 * 8;         // 8192
 constexpr int kVzTile = 2 * 64 * 8;            // 1024
 constexpr int kBuf = kKTile + kVTile + kVzTile;
 constexpr int kPKmeta = 3 * 4 * 16 * 4;        // [s | n | z][group][pair] u32, per K wave
-constexpr int kPLds = 2 * kBuf + 2 * kPKmeta;
+constexpr int kPLds = 2 * kBuf + 4 * kPKmeta;
 
 // bf16 pair (one dword) -> fp16 pair (exact for values in fp16's normal range)
 __device__ __forceinline__ uint32_t bf16x2_to_h2(uint32_t w) {
@@ -75,10 +75,11 @@ void prefill_kernel(const PrefillParams p) {
     const int r0 = rtile * kPrefillRows;
 
     // ---- token tiles of this split: hot tiles first, then warm units
-    const int64_t n_ht = (p.n_hot + kPTok - 1) / kPTok, n_wt = (p.n_warm + kPTok - 1) / kPTok;
-    const int64_t nt = n_ht + n_wt;
-    const int64_t t_begin = min((int64_t)split * p.tiles_per_split, nt);
-    const int64_t t_end = min(t_begin + p.tiles_per_split, nt);
+    const int n_ht = (int)((p.n_hot + kPTok - 1) / kPTok), n_wt = (int)((p.n_warm + kPTok - 1) / kPTok);
+    const int nt = n_ht + n_wt;
+    const int t_begin = (int)min((int64_t)split * p.tiles_per_split, (int64_t)nt);
+    const int t_end = (int)min((int64_t)t_begin + p.tiles_per_split, (int64_t)nt);
+    const int n_hot32 = (int)p.n_hot, n_warm32 = (int)p.n_warm;
 
     // ---- query operand of the wave's two column groups (rows past R repeat row r0)
     const float sl2 = p.scale_log2;
@@ -116,18 +117,23 @@ void prefill_kernel(const PrefillParams p) {
         sm[rg].accz = (f4){0.f, 0.f, 0.f, 0.f};
     }
 
-    // ---- staging roles
-    // K (waves 0, 1): token 16*wave + col of the tile, channel group grp;
-    //   meta prep: channel pair pi2 of group g2 (as in the decode kernel).
-    // V (waves 2, 3): half h = wave - 2, chunk col (8 channels), tokens 16h + 4grp + i.
-    const bool kwave = wave < 2;
+    // ---- staging roles (the tile's dequant work, split over all 8 waves)
+    // K (waves 0-3): token 16*(wave & 1) + col of the tile, channel group grp,
+    //   code pairs 8*kph .. 8*kph+7 (kph = wave >> 1); meta prep: channel
+    //   pair pi2 of group g2 (as in the decode kernel), per wave.
+    // V (waves 4-7): half vh = wave & 1, chunk col (8 channels), tokens
+    //   16vh + 4grp + 2vp + {0, 1} (vp = (wave >> 1) & 1: which pair of the
+    //   lane's MFMA token quad).
+    const bool kwave = wave < 4;
     const int ktok = 16 * (wave & 1) + col;
+    const int kph = (wave >> 1) & 1;
     const int g2 = lane >> 4, pi2 = lane & 15;
     const int kch_lo = 32 * g2 + kpair_chan<BK>(pi2, 0), kch_hi = 32 * g2 + kpair_chan<BK>(pi2, 1);
     const _Float16 nmul = (_Float16)(-magic_val(koff<BK>(pi2)));
-    const int vh = wave & 1;
+    const int vh = wave & 1, vp = (wave >> 1) & 1;
     const int gv = (8 * col) / GV;
-    unsigned char *kmeta = smem + 2 * kBuf + (wave & 1) * kPKmeta;
+    unsigned char *kmeta = smem + 2 * kBuf + (wave & 3) * kPKmeta;
+    const int tpb = p.T / kPTok;  // tiles per K block
 
     const __amdgpu_buffer_rsrc_t rkc = make_rsrc((const unsigned char *)p.kc + bh * p.n_warm * KR, (uint32_t)(p.n_warm * KR));
     const __amdgpu_buffer_rsrc_t rvc = make_rsrc((const unsigned char *)p.vc + bh * p.n_warm * VR, (uint32_t)(p.n_warm * VR));
@@ -141,35 +147,37 @@ void prefill_kernel(const PrefillParams p) {
     Masks<BK> km;
     km.init();
     Masks<BV> vmk;
-    vmk.init();
+    if (BV == BK) vmk = *(const Masks<BV> *)&km;
+    else vmk.init();
 
     // Registers of the next tile, one set for every role:
-    //   hot K: hraw[0..3] = 64 B of the token;  hot V: hraw[i] = 16 B of token i;
-    //   warm K: hraw[0] = code bytes, hraw[1] = s_lo, s_hi, z_lo, z_hi of the prep pair;
-    //   warm V: hraw[0] = the chunk's codes of tokens 0..3, hraw[1] = scales, hraw[2] = zeros.
+    //   hot K: R[0..3] = 64 B of the token;  hot V: R[i] = 16 B of token i (i < 2);
+    //   warm K: R[0] = code bytes, R[1] = s_lo, s_hi, z_lo, z_hi of the prep pair;
+    //   warm V: R[0] = codes of tokens 0, 1 and their scales, R[1][0..1] = their zeros.
     u4 hraw[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) hraw[i] = (u4){0u, 0u, 0u, 0u};
 
     // Global loads of tile t into the lane's registers (ranges past the end read 0).
-    auto load_tile = [&](int64_t t) {
+    auto load_tile = [&](int t) {
         if (t < n_ht) {
-            const int64_t tok0 = t * kPTok;
+            const uint32_t tok0 = (uint32_t)t * kPTok;
             if (kwave) {
-                const uint32_t off = (uint32_t)((tok0 + ktok) * kPD + 32 * grp) * 2u;
+                const uint32_t off = ((tok0 + ktok) * kPD + 32 * grp) * 2u;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) hraw[i] = bld128(rkh, off + 16u * i);
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t off = (uint32_t)((tok0 + 16 * vh + 4 * grp + i) * kPD + 8 * col) * 2u;
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t off = ((tok0 + 16 * vh + 4 * grp + 2 * vp + i) * kPD + 8 * col) * 2u;
                     hraw[i] = bld128(rvh, off);
                 }
             }
         } else {
-            const int64_t u = t - n_ht, tok0 = u * kPTok;
+            const int u = t - n_ht;
+            const uint32_t tok0 = (uint32_t)u * kPTok;
             if (kwave) {
-                const uint32_t off = (uint32_t)((tok0 + ktok) * KR + grp * 4 * BK);
+                const uint32_t off = (tok0 + ktok) * KR + grp * 4 * BK;
                 if (BK == 4) hraw[0] = bld128(rkc, off);
                 else if (BK == 3) {
                     const u3 x = bld96(rkc, off);
@@ -178,13 +186,13 @@ void prefill_kernel(const PrefillParams p) {
                     const u2 x = bld64(rkc, off);
                     hraw[0] = (u4){x[0], x[1], 0u, 0u};
                 }
-                const uint32_t mrow = (uint32_t)(tok0 / p.T) * kPD;
+                const uint32_t mrow = (uint32_t)(tpb == 1 ? u : u / tpb) * kPD;
                 hraw[1] = (u4){bld16(rks, (mrow + kch_lo) * 2u), bld16(rks, (mrow + kch_hi) * 2u),
                                bld16(rkz, (mrow + kch_lo) * 2u), bld16(rkz, (mrow + kch_hi) * 2u)};
             } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t tk = (uint32_t)(tok0 + 16 * vh + 4 * grp + i);
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t tk = tok0 + 16 * vh + 4 * grp + 2 * vp + i;
                     if (BV == 3) {
                         const uint32_t off = tk * VR + 3 * col;
                         const uint32_t d0 = bld32(rvc, off & ~3u);
@@ -195,15 +203,15 @@ void prefill_kernel(const PrefillParams p) {
                     } else {
                         hraw[0][i] = bld16(rvc, tk * VR + 2 * col);
                     }
-                    hraw[1][i] = bld16(rvs, (tk * NG + gv) * 2u);
-                    hraw[2][i] = bld16(rvz, (tk * NG + gv) * 2u);
+                    hraw[0][2 + i] = bld16(rvs, (tk * NG + gv) * 2u);
+                    hraw[1][i] = bld16(rvz, (tk * NG + gv) * 2u);
                 }
             }
         }
     };
 
     // Dequantize the registers of tile t into LDS buffer `buf`.
-    auto stage_tile = [&](int64_t t, unsigned char *buf) {
+    auto stage_tile = [&](int t, unsigned char *buf) {
         unsigned char *kt = buf, *vt = buf + kKTile, *vzt = buf + kKTile + kVTile;
         if (t < n_ht) {
             if (kwave) {
@@ -216,17 +224,20 @@ void prefill_kernel(const PrefillParams p) {
                         nat[4 * q4 + e] = xe;
                     }
                 hot_k_pairs<BK>(nat, pairs);
-                u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64);
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4)
-                    dst[q4] = (u4){pairs[4 * q4], pairs[4 * q4 + 1], pairs[4 * q4 + 2], pairs[4 * q4 + 3]};
+                u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64 + kph * 32);
+                if (kph == 0) {
+                    dst[0] = (u4){pairs[0], pairs[1], pairs[2], pairs[3]};
+                    dst[1] = (u4){pairs[4], pairs[5], pairs[6], pairs[7]};
+                } else {
+                    dst[0] = (u4){pairs[8], pairs[9], pairs[10], pairs[11]};
+                    dst[1] = (u4){pairs[12], pairs[13], pairs[14], pairs[15]};
+                }
             } else {
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
                     const uint32_t sel = (kk & 1) ? 0x07060302u : 0x05040100u;
-                    const uint32_t lo = perm(hraw[1][kk / 2], hraw[0][kk / 2], sel);
-                    const uint32_t hi = perm(hraw[3][kk / 2], hraw[2][kk / 2], sel);
-                    *(u2 *)(vt + ((kk * 64 + lane) * 2 + vh) * 8) = (u2){lo, hi};
+                    *(uint32_t *)(vt + ((kk * 64 + lane) * 2 + vh) * 8 + vp * 4) =
+                        perm(hraw[1][kk / 2], hraw[0][kk / 2], sel);
                 }
             }
             return;
@@ -242,85 +253,82 @@ void prefill_kernel(const PrefillParams p) {
             kmw[(1 * 4 + g2) * 16 + pi2] = as_u32(n2);
             kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
             __builtin_amdgcn_wave_barrier();
-            h2 ksc[16], kng[16], kze[16];
-            const u4 *srcm = (const u4 *)kmeta;
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-                const u4 av = srcm[(0 * 4 + grp) * 4 + q4];
-                const u4 nv = srcm[(1 * 4 + grp) * 4 + q4];
-                const u4 zv = srcm[(2 * 4 + grp) * 4 + q4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t ae = av[e], ne = nv[e], ze = zv[e];
-                    ksc[4 * q4 + e] = as_h2(ae);
-                    kng[4 * q4 + e] = as_h2(ne);
-                    kze[4 * q4 + e] = as_h2(ze);
-                }
-            }
             KWin<BK> W;
             const uint32_t kraw[4] = {hraw[0][0], hraw[0][1], hraw[0][2], hraw[0][3]};
             k_windows<BK>(kraw, W);
-            uint32_t out[16];
-            if (kfast) {
+            const u4 *srcm = (const u4 *)kmeta;
+            uint32_t out[8];
+            // pairs 8*kph + 4*c + e of this lane's group
+            auto deq = [&](int ph) {
+                if (kfast) {
 #pragma unroll
-                for (int pi = 0; pi < 16; ++pi) {
-                    const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
-                    out[pi] = as_u32(pk_fma(as_h2(uu), ksc[pi], kng[pi]) + kze[pi]);
-                }
-            } else {
+                    for (int c = 0; c < 2; ++c) {
+                        const int q4 = 2 * ph + c;
+                        const u4 av = srcm[(0 * 4 + grp) * 4 + q4];
+                        const u4 nv = srcm[(1 * 4 + grp) * 4 + q4];
+                        const u4 zv = srcm[(2 * 4 + grp) * 4 + q4];
 #pragma unroll
-                for (int pi = 0; pi < 16; ++pi) {
-                    const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
-                    const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
-                    out[pi] = as_u32((as_h2(uu) - (h2){mv, mv}) * ksc[pi] + kze[pi]);
-                }
-            }
-            u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64);
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) dst[q4] = (u4){out[4 * q4], out[4 * q4 + 1], out[4 * q4 + 2], out[4 * q4 + 3]};
-            __builtin_amdgcn_wave_barrier();  // kmeta reads done before the next tile's writes
-        } else {
-            h2 vs[2], vz[2];
-#pragma unroll
-            for (int pp = 0; pp < 2; ++pp) {
-                vs[pp] = as_h2(hraw[1][2 * pp] | (hraw[1][2 * pp + 1] << 16));
-                vz[pp] = as_h2(hraw[2][2 * pp] | (hraw[2][2 * pp + 1] << 16));
-            }
-            bool vfin = true;
-            {
-                const _Float16 n0 = (_Float16)(-1024.0f);
-                vfin = finite2(as_u32(vs[0] * (h2){n0, n0})) && finite2(as_u32(vs[1] * (h2){n0, n0}));
-            }
-            const bool vfast = !__builtin_amdgcn_ballot_w64(!vfin);
-            uint32_t vpair[2][8];
-#pragma unroll
-            for (int pp = 0; pp < 2; ++pp) {
-                uint32_t win[VSlot<BV>::NW];
-                v_windows<BV>(hraw[0][2 * pp], hraw[0][2 * pp + 1], win);
-                if (vfast) {
-                    h2 vn[v_noffs<BV>()];
-#pragma unroll
-                    for (int oi = 0; oi < v_noffs<BV>(); ++oi) {
-                        const _Float16 m = (_Float16)(-magic_val(oi * v_ostep<BV>()));
-                        vn[oi] = vs[pp] * (h2){m, m};
-                    }
-#pragma unroll
-                    for (int kk = 0; kk < 8; ++kk) {
-                        const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
-                        vpair[pp][kk] = as_u32(pk_fma(as_h2(uu), vs[pp], vn[voff<BV>(kk) / v_ostep<BV>()]));
+                        for (int e = 0; e < 4; ++e) {
+                            const int pi = 4 * q4 + e;
+                            const uint32_t ae = av[e], ne = nv[e], ze = zv[e];
+                            const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            out[4 * c + e] = as_u32(pk_fma(as_h2(uu), as_h2(ae), as_h2(ne)) + as_h2(ze));
+                        }
                     }
                 } else {
 #pragma unroll
-                    for (int kk = 0; kk < 8; ++kk) {
-                        const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
-                        const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
-                        vpair[pp][kk] = as_u32((as_h2(uu) - (h2){mv, mv}) * vs[pp]);
+                    for (int c = 0; c < 2; ++c) {
+                        const int q4 = 2 * ph + c;
+                        const u4 av = srcm[(0 * 4 + grp) * 4 + q4];
+                        const u4 zv = srcm[(2 * 4 + grp) * 4 + q4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int pi = 4 * q4 + e;
+                            const uint32_t ae = av[e], ze = zv[e];
+                            const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
+                            out[4 * c + e] = as_u32((as_h2(uu) - (h2){mv, mv}) * as_h2(ae) + as_h2(ze));
+                        }
                     }
+                }
+            };
+            if (kph == 0) deq(0);
+            else deq(1);
+            u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64 + kph * 32);
+            dst[0] = (u4){out[0], out[1], out[2], out[3]};
+            dst[1] = (u4){out[4], out[5], out[6], out[7]};
+            __builtin_amdgcn_wave_barrier();  // kmeta reads done before the next tile's writes
+        } else {
+            const h2 vs = as_h2(hraw[0][2] | (hraw[0][3] << 16));
+            const h2 vz = as_h2(hraw[1][0] | (hraw[1][1] << 16));
+            const _Float16 n0 = (_Float16)(-1024.0f);
+            const bool vfast = !__builtin_amdgcn_ballot_w64(!finite2(as_u32(vs * (h2){n0, n0})));
+            uint32_t win[VSlot<BV>::NW];
+            v_windows<BV>(hraw[0][0], hraw[0][1], win);
+            uint32_t vpair[8];
+            if (vfast) {
+                h2 vn[v_noffs<BV>()];
+#pragma unroll
+                for (int oi = 0; oi < v_noffs<BV>(); ++oi) {
+                    const _Float16 m = (_Float16)(-magic_val(oi * v_ostep<BV>()));
+                    vn[oi] = vs * (h2){m, m};
+                }
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                    const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                    vpair[kk] = as_u32(pk_fma(as_h2(uu), vs, vn[voff<BV>(kk) / v_ostep<BV>()]));
+                }
+            } else {
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                    const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                    const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
+                    vpair[kk] = as_u32((as_h2(uu) - (h2){mv, mv}) * vs);
                 }
             }
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) *(u2 *)(vt + ((kk * 64 + lane) * 2 + vh) * 8) = (u2){vpair[0][kk], vpair[1][kk]};
-            *(u2 *)(vzt + (lane * 2 + vh) * 8) = (u2){as_u32(vz[0]), as_u32(vz[1])};
+            for (int kk = 0; kk < 8; ++kk) *(uint32_t *)(vt + ((kk * 64 + lane) * 2 + vh) * 8 + vp * 4) = vpair[kk];
+            *(uint32_t *)(vzt + (lane * 2 + vh) * 8 + vp * 4) = as_u32(vz);
         }
     };
 
@@ -330,15 +338,15 @@ void prefill_kernel(const PrefillParams p) {
         stage_tile(t_begin, smem);
     }
     __syncthreads();
-    for (int64_t t = t_begin; t < t_end; ++t) {
+    for (int t = t_begin; t < t_end; ++t) {
         const int cur = (int)((t - t_begin) & 1);
         unsigned char *buf = smem + cur * kBuf;
         const bool more = t + 1 < t_end;
         if (more) load_tile(t + 1);
 
         const bool hot = t < n_ht;
-        const int64_t tok0 = (hot ? t : t - n_ht) * kPTok;
-        const int64_t ntok = hot ? p.n_hot : p.n_warm;
+        const int tok0 = (hot ? t : t - n_ht) * kPTok;
+        const int ntok = hot ? n_hot32 : n_warm32;
         const unsigned char *kt = buf, *vt = buf + kKTile, *vzt = buf + kKTile + kVTile;
         f4 sc[2][2];
 #pragma unroll
