@@ -13,10 +13,12 @@
 //   K tile  [32 tokens][4 channel groups][16 code pairs] u32, pair order of
 //           kpair_chan() (the query operand is permuted to match), exact
 //           fp16 dequant round16(round16(c*s) + z) as in the decode kernel;
-//   V tile  the PV MFMA operand as each lane reads it: [channel kk of the
-//           chunk][lane][half] u2, values round16(c*s); the zero-points
-//           enter through one more MFMA with the tile's zeros [lane][half]
-//           u2 (sum_t P z, added to every channel of the group).
+//   V tile  the PV MFMA operand, [channel kk of the chunk][half][token pair
+//           of the lane's quad][lane] u32 (each staging wave writes 64
+//           consecutive dwords; a reading lane takes its four dwords at a
+//           256-byte stride), values round16(c*s); the zero-points enter
+//           through one more MFMA with the tile's zeros [half][pair][lane]
+//           (sum_t P z, added to every channel of the group).
 // Per column group: S^T = K . Q^T for each 16-token half (4 x 16x16x32),
 // online softmax over the 32 tokens in the log2 domain (P in fp16 x 2^7),
 // O^T += V^T . P^T over the 32 tokens (8 x 16x16x32 + 1 for the zeros).
@@ -236,7 +238,7 @@ void prefill_kernel(const PrefillParams p) {
 #pragma unroll
                 for (int kk = 0; kk < 8; ++kk) {
                     const uint32_t sel = (kk & 1) ? 0x07060302u : 0x05040100u;
-                    *(uint32_t *)(vt + ((kk * 64 + lane) * 2 + vh) * 8 + vp * 4) =
+                    *(uint32_t *)(vt + (((kk * 2 + vh) * 2 + vp) * 64 + lane) * 4) =
                         perm(hraw[1][kk / 2], hraw[0][kk / 2], sel);
                 }
             }
@@ -327,8 +329,8 @@ void prefill_kernel(const PrefillParams p) {
                 }
             }
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) *(uint32_t *)(vt + ((kk * 64 + lane) * 2 + vh) * 8 + vp * 4) = vpair[kk];
-            *(uint32_t *)(vzt + (lane * 2 + vh) * 8 + vp * 4) = as_u32(vz);
+            for (int kk = 0; kk < 8; ++kk) *(uint32_t *)(vt + (((kk * 2 + vh) * 2 + vp) * 64 + lane) * 4) = vpair[kk];
+            *(uint32_t *)(vzt + ((vh * 2 + vp) * 64 + lane) * 4) = as_u32(vz);
         }
     };
 
@@ -375,12 +377,14 @@ void prefill_kernel(const PrefillParams p) {
         pop[1] = softmax32(sm[1], sc[1][0], sc[1][1], sl2);
 #pragma unroll
         for (int kk = 0; kk < 8; ++kk) {
-            const h8 a = *(const h8 *)(vt + (kk * 64 + lane) * 16);
+            const uint32_t *va = (const uint32_t *)(vt + (kk * 4 * 64 + lane) * 4);
+            const h8 a = __builtin_bit_cast(h8, (u4){va[0], va[64], va[128], va[192]});
             sm[0].acc[kk] = mfma_k32(a, pop[0], sm[0].acc[kk]);
             sm[1].acc[kk] = mfma_k32(a, pop[1], sm[1].acc[kk]);
         }
         if (!hot) {
-            const h8 az = *(const h8 *)(vzt + lane * 16);
+            const uint32_t *za = (const uint32_t *)(vzt + lane * 4);
+            const h8 az = __builtin_bit_cast(h8, (u4){za[0], za[64], za[128], za[192]});
             sm[0].accz = mfma_k32(az, pop[0], sm[0].accz);
             sm[1].accz = mfma_k32(az, pop[1], sm[1].accz);
         }
