@@ -699,16 +699,17 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
 // f_s = exp2(m_s - M).  One workgroup of 256 threads per (batch, kv-head, chunk,
 // row): thread = (channel quad q, split lane sl); each thread keeps its splits'
 // float4 loads in flight, the split lanes are summed through LDS.
+// Merge the split partials (m, l, acc) of one query row: row rr of 16-row
+// chunk bhc % nchunk of (batch, kv-head) bhc / nchunk, into the output (and
+// the row statistics when p.rowstats).  Thread (split lane sl, channel quad
+// q) walks splits sl, sl + SL, ... in batches of KB whose loads are all in
+// flight together, merging them online (log-sum-exp); the SL lanes then merge
+// through LDS.  At <= SL*KB splits the whole merge costs one round trip to
+// memory.  256 threads.
 template <int D>
-__global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p) {
-    // Thread (split lane sl, channel quad q) walks splits sl, sl + SL, ... in
-    // batches of KB whose loads are all in flight together, merging them
-    // online (log-sum-exp); the SL lanes then merge through LDS.  At <= SL*KB
-    // splits the whole merge costs one round trip to memory.
+__device__ __forceinline__ void merge_split_row(const DecodeParams &p, int bhc, int rr, float *sm, float *sls,
+                                                f4 (*accl)[D / 4]) {
     constexpr int NQ = D / 4, SL = 256 / NQ, PS = D + 4, KB = 4;
-    __shared__ float sm[SL], sls[SL];
-    __shared__ f4 accl[SL][NQ];
-    const int bhc = blockIdx.x, rr = blockIdx.y;
     const int chunk = bhc % p.nchunk;
     const int64_t bh = bhc / p.nchunk;
     const int b = (int)(bh / p.Hkv), kvh = (int)(bh % p.Hkv);
@@ -787,6 +788,13 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p
     }
 }
 
+template <int D>
+__global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p) {
+    __shared__ float sm[256 / (D / 4)], sls[256 / (D / 4)];
+    __shared__ f4 accl[256 / (D / 4)][D / 4];
+    merge_split_row<D>(p, blockIdx.x, blockIdx.y, sm, sls, accl);
+}
+
 // Normalise the stashed log2-domain logits into attention weights and/or
 // accumulate the importance EMA.  Workgroup = 64 tokens x 16 row lanes: thread
 // (token t, row lane rl) walks rows rl, rl+16, ... for tokens t, t+16, t+32,
@@ -825,6 +833,112 @@ __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodePar
             // mean over (batch, head), summed over query positions
             float sc = p.scores[n] * p.decay;
             sc = sc + s / (float)(p.B * p.Hq);
+            p.scores[n] = sc;
+        }
+    }
+}
+
+// Split merge + attention weights / importance EMA in one launch (the stash
+// path).  Every workgroup first rebuilds the statistics of every query row
+// from the split partials -- M = max_s m_s, L = sum_s 2^(m_s - M) l_s (x 2^7)
+// -- into LDS; workgroup i < B*Hkv*nchunk*prows also merges the output of one
+// row (as decode_reduce_kernel); then each workgroup normalises 64 tokens of
+// every row, w = 2^(s - M) * 128 / L, writes them when the weights are asked
+// for and adds sum_rows w / (B*Hq) to the importance EMA.  Loads of a phase
+// are issued together.  Needs rows <= kFinishRows.
+constexpr int kFinishRows = 1024;
+
+template <int D>
+__global__ __launch_bounds__(256) void finish_kernel(const DecodeParams p) {
+    __shared__ float sm[256 / (D / 4)], sls[256 / (D / 4)];
+    __shared__ f4 accl[256 / (D / 4)][D / 4];
+    __shared__ float rM[kFinishRows], rW[kFinishRows];
+    __shared__ float red[16][65];
+    const int tid = threadIdx.x;
+    const int rows = p.B * p.Hq * p.M;
+    const int ns = p.nsplit;
+    const int64_t PS = D + 4;
+    const int64_t pstride = (int64_t)p.prows * PS;
+
+    // output merge of one (chunk, row)
+    const int n_merge = p.B * p.Hkv * p.nchunk * p.prows;
+    if ((int)blockIdx.x < n_merge)
+        merge_split_row<D>(p, blockIdx.x / p.prows, blockIdx.x % p.prows, sm, sls, accl);
+
+    // statistics of every row, one thread per row with all its split loads in flight
+    for (int r = tid; r < rows; r += 256) {
+        const int b = r / (p.Hq * p.M), hm = r % (p.Hq * p.M);
+        const int h = hm / p.M, m = hm % p.M;
+        const int kvh = h / p.g, rk = (h % p.g) * p.M + m;  // row within the kv-head's g*M rows
+        const float *pp = p.part + ((int64_t)(b * p.Hkv + kvh) * p.nchunk + rk / 16) * ns * pstride + (rk % 16) * PS;
+        float M = -INFINITY, L = 0.f;
+        for (int s0 = 0; s0 < ns; s0 += 16) {
+            float ms[16], ls[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                ms[k] = s0 + k < ns ? pp[(int64_t)(s0 + k) * pstride] : -INFINITY;
+                ls[k] = s0 + k < ns ? pp[(int64_t)(s0 + k) * pstride + 1] : 0.f;
+            }
+            float nm = M;
+#pragma unroll
+            for (int k = 0; k < 16; ++k) nm = fmaxf(nm, ms[k]);
+            if (nm == -INFINITY) continue;
+            L *= (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - nm);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) L += (ms[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[k] - nm) * ls[k];
+            M = nm;
+        }
+        rM[r] = M;
+        rW[r] = 128.0f / L;  // undo the 2^7 probability scale
+    }
+    __syncthreads();
+
+    // weights and importance of tokens 64*blockIdx.x .. +63
+    const int64_t N = p.N;
+    const int64_t nmax = N > p.n_scores ? N : p.n_scores;
+    if ((int64_t)blockIdx.x * 64 >= nmax) return;
+    const int t = tid & 15, rl = tid >> 4;
+    const int64_t n0 = (int64_t)blockIdx.x * 64 + t;
+    float imp[4] = {0.f, 0.f, 0.f, 0.f};
+    constexpr int RB = 8;  // rows per batch of loads
+    for (int r0 = rl; r0 < rows; r0 += 16 * RB) {
+        float x[RB][4];
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + 16 * j;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                x[j][i] = (r < rows && n0 + 16 * i < N) ? p.stash[(int64_t)r * N + n0 + 16 * i] : -INFINITY;
+        }
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int r = r0 + 16 * j;
+            if (r >= rows) break;
+            const float M = rM[r], W = rW[r];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[j][i] - M);
+                const float wgt = e * W;
+                if (n0 + 16 * i < N) {
+                    if (p.attn_out) p.stash[(int64_t)r * N + n0 + 16 * i] = wgt;
+                    imp[i] += wgt;
+                }
+            }
+        }
+    }
+    if (!p.scores) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[rl][16 * i + t] = imp[i];
+    __syncthreads();
+    if (tid < 64) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) sacc += red[k][tid];
+        const int64_t n = (int64_t)blockIdx.x * 64 + tid;
+        if (n < p.n_scores) {
+            // mean over (batch, head), summed over query positions
+            float sc = p.scores[n] * p.decay;
+            sc = sc + sacc / (float)(p.B * p.Hq);
             p.scores[n] = sc;
         }
     }
@@ -902,6 +1016,16 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
     if (decode_fast_eligible(p, wk)) e = decode_fast_split_launch(p, kb, vb, s);
     else e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
+    const int64_t rows = (int64_t)p.B * p.Hq * p.M;
+    if (p.stash && rows <= kFinishRows) {
+        // one launch: output merge + weights / importance
+        const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
+        const int64_t n_tok = (nmax + 63) / 64, n_merge = (int64_t)p.B * p.Hkv * p.nchunk * p.prows;
+        const unsigned nwg = (unsigned)(n_tok > n_merge ? n_tok : n_merge);
+        if (p.D == 64) hipLaunchKernelGGL(finish_kernel<64>, dim3(nwg), dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(finish_kernel<128>, dim3(nwg), dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
     if ((e = decode_reduce_launch(p, s)) != hipSuccess) return e;
     if (p.stash) {
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
