@@ -10,9 +10,18 @@ Workload (one step = one decode token through all 28 layers): batch 8,
 step is captured once in a HIP graph and replayed.
 
 Prints one JSON line: value = effective KV GB/s (hot + warm codes + scale /
-zero bytes read per layer / time per layer), plus us_per_layer, the
-roofline of the fused decode op and the CPU baseline (the oracle's
-restatement of the reference CPU path on a bounded sample).
+zero bytes read per layer / time per layer, the full step with importance),
+plus us_per_layer, the roofline of the dequant-attention op and the CPU
+baseline (the oracle's restatement of the reference CPU path on a bounded
+sample).
+
+The roofline is taken on the attention-only replay (per layer: the split
+kernel decode_fast_kernel, which carries ~85% of the time, and the split
+merge): achieved = the op's algorithmic bytes / its per-layer time, from HIP
+events on the stream the kernels run on.  `traffic` (HBM bytes per layer of
+that op) comes from the FETCH_SIZE / WRITE_SIZE counter runs recorded in
+profiles/decode_qwen_decode_32k_traffic.json, scaled by the same counters on
+a copy of known size (--calib-copy adds that copy to the run).
 """
 from __future__ import annotations
 
@@ -27,6 +36,8 @@ sys.path.insert(0, os.path.join(ROOT, "adaptive-kv-memory_amd"))
 
 METRIC = "decode-attn µs/layer + effective KV GB/s (% HBM peak) at 32K ctx, 1×MI355X"
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_qwen_decode_32k_traffic.json")
+CALIB_BYTES = 256 << 20  # the calibration copy reads and writes this many bytes
 
 
 def layer_bytes(s):
@@ -83,6 +94,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--layers", type=int, default=0, help="override layer count (profiling only)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="end with one device copy of 256 MiB (reference dispatch for counter runs)")
+    ap.add_argument("--workload", default="qwen_decode_32k",
+                    choices=["qwen_decode_32k", "llama70b_prefill_128k", "llama3_demote_64k"],
+                    help="the headline decode step (default), or the chunked prefill / demotion workloads")
+    ap.add_argument("--bits", type=int, default=3, help="demotion workload: code width (2, 3 or 4)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU; the warm-tier path has no multi-GPU leg "
@@ -93,6 +110,10 @@ def main():
     import akv
     from akv import workloads as wl
     from akv.warm_tier import DecodeCall
+    if args.workload == "llama70b_prefill_128k":
+        return bench_prefill(args)
+    if args.workload == "llama3_demote_64k":
+        return bench_demote(args)
 
     s = wl.QWEN_DECODE_32K
     L = args.layers or s.layers
@@ -144,8 +165,12 @@ def main():
     us_layer = ev_ms * 1e3 / L
     us_layer_attn = ev_attn_ms * 1e3 / L
     kv_gbps = nb["kv"] / (us_layer * 1e-6) / 1e9
-    alg = nb["attn_total"] + nb["importance"]
-    achieved = alg / (us_layer * 1e-6) / 1e9
+    alg = nb["attn_total"]
+    achieved = alg / (us_layer_attn * 1e-6) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_layer_attn")
     res = {
         "metric": METRIC,
         "value": round(kv_gbps, 2),
@@ -167,13 +192,148 @@ def main():
         "effective_kv_gbps_attn_only": round(nb["kv"] / (us_layer_attn * 1e-6) / 1e9, 2),
         "hbm_frac_effective_kv": round(kv_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "akv_decode_attn (split + reduce + importance) per layer",
-                     "algorithmic_bytes_per_launch": alg},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "kernel": "akv_decode_attn attention per layer (decode_fast_kernel + decode_reduce_kernel)",
+                     "algorithmic_bytes_per_launch": alg,
+                     "us_per_launch": round(us_layer_attn, 3)},
     }
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(layers[0], s)
+    if args.calib_copy:
+        src = torch.zeros(CALIB_BYTES // 2, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)  # one elementwise kernel: reads and writes CALIB_BYTES
+        torch.cuda.synchronize()
+    print(json.dumps(res), flush=True)
+
+
+def _event_time(fn, steps, warmup):
+    """Average ms of fn() over `steps` calls after `warmup`, HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps, (time.perf_counter() - t0) * 1e3 / steps
+
+
+def bench_prefill(args):
+    """Chunked prefill, Llama-3-70B attention shape: 512 bf16 queries x 64 heads over
+    131072 cached tokens (4096 hot fp16 + 126976 warm at 2/2 bits), batch 1."""
+    import numpy as np
+    import torch
+    import akv
+    from akv import workloads as wl
+    from threadpoolctl import threadpool_limits
+    from oracle import affine as oaff
+    from oracle import attention as oatt
+    s = wl.LLAMA70B_PREFILL_128K
+    print(f"[bench] building {s.name}", file=sys.stderr, flush=True)
+    k, v = wl.make_kv(s, device="cuda")
+    q = wl.make_q(s, device="cuda", dtype=torch.bfloat16)
+    (kw, vw), (kh, vh) = wl.split_hot_warm(k, v, s.n_hot)
+    warm = akv.quantize_kv(kw, vw, s.bits_k, s.bits_v, s.block_t, s.group_v)
+    del k, v, kw, vw
+    torch.cuda.synchronize()
+    ms, wall_ms = _event_time(lambda: akv.prefill_attention(q, kh, vh, warm), args.steps, args.warmup)
+    flops = 4.0 * s.Hq * s.M * s.N * s.D * s.B
+    tflops = flops / (ms * 1e-3) / 1e12
+    res = {"metric": "chunked-prefill attention TFLOP/s at 128K ctx (Llama-3-70B shape), 1xMI355X",
+           "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(wall_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f16", "data": "synthetic (seeded N(0,1) K/V, bf16 queries, quantized on the device)",
+           "config": {"workload": s.name, "B": s.B, "Hq": s.Hq, "Hkv": s.Hkv, "D": s.D, "M": s.M,
+                      "context": s.N, "n_hot": s.n_hot, "n_warm": s.n_warm, "bits_k": s.bits_k, "bits_v": s.bits_v},
+           "ms_per_call": round(ms, 4),
+           "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
+                        "frac": round(tflops / 2500.0, 4), "traffic": None,
+                        "kernel": "prefill_kernel (one launch at this shape)", "flops_per_launch": flops}}
+    if not args.no_cpu_baseline:
+        # oracle: dequant + fp32 attention of kv-head 0's 8 query heads at 16 positions
+        host = {n: getattr(warm, n)[:, :1].cpu().numpy() for n in ("k_codes", "k_scale", "k_zero",
+                                                                    "v_codes", "v_scale", "v_zero")}
+        host.update(bits_k=s.bits_k, bits_v=s.bits_v, T=s.block_t, G=s.group_v, D=s.D, N=s.n_warm, n_out=0)
+        g = s.Hq // s.Hkv
+        qs = q[:, :g, :16].float().cpu().numpy()
+        khn, vhn = kh[:, :1].cpu().numpy(), vh[:, :1].cpu().numpy()
+        cores = len(os.sched_getaffinity(0))
+        with threadpool_limits(limits=cores):
+            t0 = time.perf_counter()
+            kd, vd = oaff.dequant_kv_blocked(host)
+            oatt.mixed_attention_fp32(qs, khn, vhn, kd, vd, return_weights=False)
+            t_cpu = time.perf_counter() - t0
+        f_cpu = 4.0 * g * 16 * s.N * s.D
+        res["cpu_baseline"] = {"value": round(f_cpu / t_cpu / 1e12, 6), "unit": "TFLOP/s", "cores": cores,
+                               "kind": "port", "sample": f"kv-head 0, 8 query heads x 16 positions: dequant + fp32 "
+                                                         f"attention over 131072 tokens, {t_cpu:.1f} s"}
+    print(json.dumps(res), flush=True)
+
+
+def bench_demote(args):
+    """Demotion: Llama-3-8B GQA shape, 16 x 8 kv-heads x 65536 fp16 tokens; the
+    64512 least important tokens per sequence (first 4 and last 16 protected)
+    are selected on the device, gathered, quantized per 32-token block and packed."""
+    import torch
+    import akv
+    from akv import workloads as wl
+    from akv.drop_in import select_demote_indices
+    from threadpoolctl import threadpool_limits
+    from oracle import affine as oaff
+    s = wl.LLAMA3_DEMOTE_64K
+    bits = args.bits
+    print(f"[bench] building {s.name}", file=sys.stderr, flush=True)
+    k, v, imp = wl.make_demote_inputs(s, device="cuda")
+    n = s.S - s.keep_hot
+    torch.cuda.synchronize()
+
+    def step():
+        sel = select_demote_indices(imp, n, s.S, s.hot_budget)
+        return akv.quantize_kv(k, v, bits, bits, s.block_t, s.group_v, sel=sel)
+
+    ms, wall_ms = _event_time(step, args.steps, args.warmup)
+    sel_fixed = select_demote_indices(imp, n, s.S, s.hot_budget)
+    ms_q, _ = _event_time(lambda: akv.quantize_kv(k, v, bits, bits, s.block_t, s.group_v, sel=sel_fixed),
+                          args.steps, 1)
+    from akv.warm_tier import packed_row_bytes
+    nblk = (n + s.block_t - 1) // s.block_t
+    rd = s.B * s.H * n * s.D * 2 * 2 + s.B * s.S * 4
+    wr = (s.B * s.H * n * packed_row_bytes(s.D, bits) * 2 + s.B * s.H * nblk * s.D * 2 * 2
+          + s.B * s.H * n * (s.D // s.group_v) * 2 * 2 + s.B * n * 8)
+    gbps = (rd + wr) / (ms * 1e-3) / 1e9
+    res = {"metric": f"demotion quantize+bitpack GB/s at 64K tokens (Llama-3-8B GQA, {bits}-bit), 1xMI355X",
+           "value": round(gbps, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(wall_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "dtype": "f16", "data": "synthetic (seeded N(0,1) fp16 K/V, importance U(0,1))",
+           "config": {"workload": s.name, "B": s.B, "H": s.H, "D": s.D, "S": s.S, "demoted": n, "bits": bits,
+                      "block_t": s.block_t, "group_v": s.group_v},
+           "ms_per_call": round(ms, 4),
+           "ms_quantize_only": round(ms_q, 4),
+           "roofline": {"bound": "hbm", "achieved": round((rd + wr) / (ms_q * 1e-3) / 1e9, 2),
+                        "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round((rd + wr) / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "kernel": "quant_kernel (gather + quantize + pack, one launch)",
+                        "algorithmic_bytes_per_launch": rd + wr}}
+    if not args.no_cpu_baseline:
+        import numpy as np
+        cores = len(os.sched_getaffinity(0))
+        sel0 = select_demote_indices(imp[:1], n, s.S, s.hot_budget)[0].cpu().numpy()
+        kb = k[:1, :, sel0[:8192]].cpu().numpy()
+        vb = v[:1, :, sel0[:8192]].cpu().numpy()
+        with threadpool_limits(limits=cores):
+            t0 = time.perf_counter()
+            oaff.quantize_kv_blocked(kb, vb, bits, bits, s.block_t, s.group_v)
+            t_cpu = time.perf_counter() - t0
+        b_cpu = (rd + wr) * (8192 / n) / s.B
+        res["cpu_baseline"] = {"value": round(b_cpu / t_cpu / 1e9, 4), "unit": "GB/s", "cores": cores,
+                               "kind": "port", "sample": f"sequence 0, 8 kv-heads x 8192 selected tokens "
+                                                         f"(quantize + pack), {t_cpu:.1f} s"}
     print(json.dumps(res), flush=True)
 
 
