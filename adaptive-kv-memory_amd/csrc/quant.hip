@@ -287,6 +287,261 @@ __global__ __launch_bounds__(256) void quant_kernel(const QuantParams p) {
     }
 }
 
+// ---------------------------------------------------------------- fast path
+// fp16 input and arithmetic, D = 128, K per channel over 32-token blocks, V per
+// token over G-channel groups, no outliers: one wave per (batch, head, block).
+// Lane (cg = lane % 16, tg = lane / 16) holds channels 8cg .. 8cg+7 of the
+// block's tokens 8tg .. 8tg+7 (one 16-byte load per token and tensor).
+//   min / max: packed fp16 min / max in the lane, then across the lanes that
+//   share a channel (K: the 4 token groups) or a group (V: G/8 channel groups);
+//   scale = round16(round16(max - min) * (1/maxv)) -- equal to the reference's
+//   division by maxv for every fp16 value, checked exhaustively;
+//   code = clamp(rint(round16(round16(x - zero) / scale)), 0, maxv) computed as
+//   one fused multiply by r = 1/scale (fp32, correctly rounded) rounded once
+//   to fp16 (v_fma_mix), then + 1024 (fp16 rounding to an integer, ties to
+//   even) and a clamp in [1024, 1024 + maxv]: the same codes as the
+//   reference for every fp16 quotient, checked exhaustively over all fp16
+//   (x - zero, scale) pairs; NaN gives 0 and +inf gives maxv as there.
+// Packed rows go through LDS and leave as one contiguous 16-byte-per-lane
+// store per tensor (a block's rows are contiguous in the packed layout).
+
+namespace {
+
+// fp16 of a * r (r fp32) with one rounding, for the low / high half of a.
+__device__ __forceinline__ uint32_t mul_mix2(uint32_t a, float r_lo, float r_hi) {
+    uint32_t d = 0;
+    asm volatile("v_fma_mixlo_f16 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "+v"(d) : "v"(a), "v"(r_lo));
+    asm volatile("v_fma_mixhi_f16 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(d) : "v"(a), "v"(r_hi));
+    return d;
+}
+
+// codes of a pair of quotients d (fp16x2): (1024 + code) in each half
+__device__ __forceinline__ uint32_t code2(uint32_t d, h2 hi_clamp) {
+    const h2 k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+    h2 u = as_h2(d) + k1024;
+    u = __builtin_elementwise_max(u, k1024);
+    u = __builtin_elementwise_min(u, hi_clamp);
+    return as_u32(u);
+}
+
+__device__ __forceinline__ h2 hmin2(h2 a, h2 b) { return __builtin_elementwise_min(a, b); }
+__device__ __forceinline__ h2 hmax2(h2 a, h2 b) { return __builtin_elementwise_max(a, b); }
+
+// scale of a (min, max) pair held as fp16: round16(round16(mx - mn) * (1/maxv))
+__device__ __forceinline__ float scale_of(_Float16 mn, _Float16 mx, float inv_maxv) {
+    const _Float16 d = mx - mn;
+    return (float)(_Float16)((float)d * inv_maxv);
+}
+
+// packed bytes of 8 codes (held as 1024 + code in the fp16 halves of c[0..3])
+template <int BITS>
+__device__ __forceinline__ void pack_row(const uint32_t *c, unsigned char *dst) {
+    uint32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = c[i] & 0x3FFu;
+        v[2 * i + 1] = (c[i] >> 16) & 0x3FFu;
+    }
+    if (BITS == 4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w |= ((v[2 * i] << 4) | v[2 * i + 1]) << (8 * i);
+        *(uint32_t *)dst = w;
+    } else if (BITS == 2) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) w |= ((v[4 * i] << 6) | (v[4 * i + 1] << 4) | (v[4 * i + 2] << 2) | v[4 * i + 3]) << (8 * i);
+        *(uint16_t *)dst = (uint16_t)w;
+    } else {
+        uint32_t W = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) W |= v[i] << (21 - 3 * i);
+        dst[0] = (unsigned char)(W >> 16);
+        dst[1] = (unsigned char)(W >> 8);
+        dst[2] = (unsigned char)W;
+    }
+}
+
+template <int N>
+__device__ __forceinline__ uint32_t xor_lane(uint32_t x) { return (uint32_t)__shfl_xor((int)x, N); }
+
+}  // namespace
+
+template <int BK, int BV, int NG>
+__global__ __launch_bounds__(256) void quant_fast_kernel(const QuantParams p) {
+    constexpr int KR = 16 * BK, VR = 16 * BV, LG = 16 / NG;  // lanes (channel groups of 8) per V group
+    __shared__ __align__(16) unsigned char stage[4][2][32 * 64 + 2 * 32 * 4 * 2];  // codes, then V meta
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + wave;
+    const int h = blockIdx.y, b = blockIdx.z;
+    if (blk >= p.nblk) return;
+    const int cg = lane & 15, tg = lane >> 4;
+    const int64_t t0 = blk * 32;
+    const int nv = (int)min((int64_t)32, p.n_sel - t0);  // valid tokens of the block
+    const int64_t bh = (int64_t)b * p.H + h;
+
+    // ---- loads: tokens 8tg + i (invalid ones repeat token t0: min / max unchanged)
+    u4 kx[8], vx[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int tl = 8 * tg + i;
+        const int64_t t = t0 + (tl < nv ? tl : 0);
+        const int64_t src = p.sel ? min(max(p.sel[(int64_t)b * p.n_sel + t], (int64_t)0), p.n_src - 1) : t;
+        const int64_t off = (bh * p.n_src + src) * 128 + 8 * cg;
+        if (p.k) kx[i] = *(const u4 *)((const _Float16 *)p.k + off);
+        if (p.v) vx[i] = *(const u4 *)((const _Float16 *)p.v + off);
+    }
+
+    // ---------------------------------------------------------------- K
+    if (p.k) {
+        constexpr int MAXV = (1 << BK) - 1;
+        const float inv = 1.0f / (float)MAXV;
+        h2 mn[4], mx[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mn[j] = mx[j] = as_h2(kx[0][j]);
+#pragma unroll
+        for (int i = 1; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                mn[j] = hmin2(mn[j], as_h2(kx[i][j]));
+                mx[j] = hmax2(mx[j], as_h2(kx[i][j]));
+            }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            mn[j] = hmin2(mn[j], as_h2(xor_lane<16>(as_u32(mn[j]))));
+            mx[j] = hmax2(mx[j], as_h2(xor_lane<16>(as_u32(mx[j]))));
+            mn[j] = hmin2(mn[j], as_h2(xor_lane<32>(as_u32(mn[j]))));
+            mx[j] = hmax2(mx[j], as_h2(xor_lane<32>(as_u32(mx[j]))));
+        }
+        float r[8];
+        uint32_t sc[4], nz[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float s0 = scale_of(mn[j][0], mx[j][0], inv), s1 = scale_of(mn[j][1], mx[j][1], inv);
+            r[2 * j] = 1.0f / s0;
+            r[2 * j + 1] = 1.0f / s1;
+            sc[j] = as_u32((h2){(_Float16)s0, (_Float16)s1});
+            nz[j] = as_u32(mn[j]) ^ 0x80008000u;  // -zero
+        }
+        if (tg == 0) {
+            const int64_t mi = (bh * p.nblk + blk) * 128 + 8 * cg;
+            *(u4 *)((_Float16 *)p.k_scale + mi) = (u4){sc[0], sc[1], sc[2], sc[3]};
+            *(u4 *)((_Float16 *)p.k_zero + mi) = (u4){as_u32(mn[0]), as_u32(mn[1]), as_u32(mn[2]), as_u32(mn[3])};
+        }
+        const h2 hic = {(_Float16)(1024.0f + MAXV), (_Float16)(1024.0f + MAXV)};
+        unsigned char *st = stage[wave][0];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            uint32_t c[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const uint32_t q = as_u32(as_h2(kx[i][j]) + as_h2(nz[j]));
+                c[j] = code2(mul_mix2(q, r[2 * j], r[2 * j + 1]), hic);
+            }
+            pack_row<BK>(c, st + (8 * tg + i) * KR + cg * BK);
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int nbytes = nv * KR;
+        unsigned char *dst = (unsigned char *)p.k_codes + (bh * p.n_sel + t0) * KR;
+        for (int o = 16 * lane; o < nbytes; o += 1024) *(u4 *)(dst + o) = *(const u4 *)(st + o);
+    }
+
+    // ---------------------------------------------------------------- V
+    if (p.v) {
+        constexpr int MAXV = (1 << BV) - 1;
+        const float inv = 1.0f / (float)MAXV;
+        // per token: min / max over the lane's 8 channels, packed two tokens per h2
+        h2 mn2[4], mx2[4];
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+            _Float16 lo_mn, lo_mx, hi_mn, hi_mx;
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const u4 x = vx[2 * i2 + e];
+                h2 a = hmin2(hmin2(as_h2(x[0]), as_h2(x[1])), hmin2(as_h2(x[2]), as_h2(x[3])));
+                h2 c = hmax2(hmax2(as_h2(x[0]), as_h2(x[1])), hmax2(as_h2(x[2]), as_h2(x[3])));
+                const _Float16 m0 = __builtin_fminf16(a[0], a[1]), m1 = __builtin_fmaxf16(c[0], c[1]);
+                if (e == 0) { lo_mn = m0; lo_mx = m1; } else { hi_mn = m0; hi_mx = m1; }
+            }
+            mn2[i2] = (h2){lo_mn, hi_mn};
+            mx2[i2] = (h2){lo_mx, hi_mx};
+        }
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+            if (LG >= 2) {
+                mn2[i2] = hmin2(mn2[i2], as_h2(xor_lane<1>(as_u32(mn2[i2]))));
+                mx2[i2] = hmax2(mx2[i2], as_h2(xor_lane<1>(as_u32(mx2[i2]))));
+            }
+            if (LG >= 4) {
+                mn2[i2] = hmin2(mn2[i2], as_h2(xor_lane<2>(as_u32(mn2[i2]))));
+                mx2[i2] = hmax2(mx2[i2], as_h2(xor_lane<2>(as_u32(mx2[i2]))));
+            }
+            if (LG >= 8) {
+                mn2[i2] = hmin2(mn2[i2], as_h2(xor_lane<4>(as_u32(mn2[i2]))));
+                mx2[i2] = hmax2(mx2[i2], as_h2(xor_lane<4>(as_u32(mx2[i2]))));
+            }
+            if (LG >= 16) {
+                mn2[i2] = hmin2(mn2[i2], as_h2(xor_lane<8>(as_u32(mn2[i2]))));
+                mx2[i2] = hmax2(mx2[i2], as_h2(xor_lane<8>(as_u32(mx2[i2]))));
+            }
+        }
+        const int gv = cg / LG;
+        unsigned char *st = stage[wave][1];
+        unsigned char *mst = st + 32 * 64;  // [token][group] scale then zero, fp16
+        const h2 hic = {(_Float16)(1024.0f + MAXV), (_Float16)(1024.0f + MAXV)};
+#pragma unroll
+        for (int i2 = 0; i2 < 4; ++i2) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int i = 2 * i2 + e, tl = 8 * tg + i;
+                const _Float16 zmn = mn2[i2][e];
+                const float s = scale_of(zmn, mx2[i2][e], inv);
+                const float r = 1.0f / s;
+                if (cg % LG == 0) {
+                    ((_Float16 *)mst)[tl * NG + gv] = (_Float16)s;
+                    ((_Float16 *)mst)[32 * NG + tl * NG + gv] = zmn;
+                }
+                const h2 nzz = {(_Float16)(-zmn), (_Float16)(-zmn)};
+                uint32_t c[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t q = as_u32(as_h2(vx[i][j]) + nzz);
+                    c[j] = code2(mul_mix2(q, r, r), hic);
+                }
+                pack_row<BV>(c, st + tl * VR + cg * BV);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        const int nbytes = nv * VR;
+        unsigned char *dst = (unsigned char *)p.v_codes + (bh * p.n_sel + t0) * VR;
+        for (int o = 16 * lane; o < nbytes; o += 1024) *(u4 *)(dst + o) = *(const u4 *)(st + o);
+        // meta: nv tokens x NG fp16 scales, then zeros (contiguous per block)
+        const int mh = nv * NG;
+        _Float16 *ds = (_Float16 *)p.v_scale + (bh * p.n_sel + t0) * NG;
+        _Float16 *dz = (_Float16 *)p.v_zero + (bh * p.n_sel + t0) * NG;
+        for (int o = lane; o < mh; o += 64) {
+            ds[o] = ((const _Float16 *)mst)[o];
+            dz[o] = ((const _Float16 *)mst)[32 * NG + o];
+        }
+    }
+}
+
+static bool quant_fast_eligible(const QuantParams &p) {
+    const bool al = (((uintptr_t)p.k | (uintptr_t)p.v | (uintptr_t)p.k_codes | (uintptr_t)p.v_codes |
+                      (uintptr_t)p.k_scale | (uintptr_t)p.k_zero) & 15u) == 0;
+    return al && p.in_dt == AKV_DT_F16 && p.ar_dt == AKV_DT_F16 && p.D == 128 && p.pD == 128 && p.T == 32 &&
+           p.k_mode == 0 && p.n_out == 0 && !p.symmetric && p.meta_dt == AKV_DT_F16 &&
+           p.bits_k >= 2 && p.bits_k <= 4 && p.bits_v >= 2 && p.bits_v <= 4 &&
+           p.sbits_k == p.bits_k && p.sbits_v == p.bits_v && (p.G_v == 32 || p.G_v == 64 || p.G_v == 128);
+}
+
+template <int BK, int BV>
+static void launch_quant_fast(const QuantParams &p, dim3 grid, hipStream_t s) {
+    if (p.G_v == 32) hipLaunchKernelGGL((quant_fast_kernel<BK, BV, 4>), grid, dim3(256), 0, s, p);
+    else if (p.G_v == 64) hipLaunchKernelGGL((quant_fast_kernel<BK, BV, 2>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((quant_fast_kernel<BK, BV, 1>), grid, dim3(256), 0, s, p);
+}
+
 hipError_t quant_launch(const QuantParams &p, hipStream_t s) {
     hipError_t e;
     if (p.n_out > 0) {
@@ -295,6 +550,14 @@ hipError_t quant_launch(const QuantParams &p, hipStream_t s) {
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     dim3 grid((unsigned)((p.nblk + 3) / 4), p.H, p.B);
+    if (quant_fast_eligible(p)) {
+#define AKV_QKV(a, c) \
+    if (p.bits_k == a && p.bits_v == c) launch_quant_fast<a, c>(p, grid, s);
+        AKV_QKV(2, 2) AKV_QKV(2, 3) AKV_QKV(2, 4) AKV_QKV(3, 2) AKV_QKV(3, 3) AKV_QKV(3, 4) AKV_QKV(4, 2)
+        AKV_QKV(4, 3) AKV_QKV(4, 4)
+#undef AKV_QKV
+        return hipGetLastError();
+    }
     if (p.ar_dt == AKV_DT_F16) hipLaunchKernelGGL(quant_kernel<AKV_DT_F16>, grid, dim3(256), 0, s, p);
     else if (p.ar_dt == AKV_DT_BF16) hipLaunchKernelGGL(quant_kernel<AKV_DT_BF16>, grid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(quant_kernel<AKV_DT_F32>, grid, dim3(256), 0, s, p);

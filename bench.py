@@ -318,7 +318,7 @@ def bench_demote(args):
            "roofline": {"bound": "hbm", "achieved": round((rd + wr) / (ms_q * 1e-3) / 1e9, 2),
                         "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round((rd + wr) / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
-                        "kernel": "quant_kernel (gather + quantize + pack, one launch)",
+                        "kernel": "quant_fast_kernel (gather + quantize + pack, one launch)",
                         "algorithmic_bytes_per_launch": rd + wr}}
     if not args.no_cpu_baseline:
         import numpy as np

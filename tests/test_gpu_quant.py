@@ -47,6 +47,17 @@ def test_blocked_quant_bit_exact(bk, bv):
     _check_warm(wt, ref)
 
 
+@pytest.mark.parametrize("G,bk,bv,N", [(64, 3, 4, 257), (128, 2, 3, 96), (32, 4, 3, 5)])
+def test_fast_path_group_sizes(G, bk, bv, N):
+    """fp16, D = 128, 32-token K blocks: the one-wave-per-block kernel for every V group size."""
+    import akv
+    announce(f"quantize_kv fast path G={G} bits={bk}/{bv} N={N}")
+    k, v = _kv(2, 3, N, 128, seed=G + N)
+    ref = oaff.quantize_kv_blocked(k, v, bk, bv, T=32, G=G)
+    wt = akv.quantize_kv(to_dev(k), to_dev(v), bk, bv, block_t=32, group_v=G)
+    _check_warm(wt, ref)
+
+
 @pytest.mark.parametrize("T,G,D", [(16, 64, 128), (64, 128, 128), (32, 32, 64), (48, 64, 64)])
 def test_block_and_group_sizes(T, G, D):
     import akv
