@@ -58,13 +58,16 @@ def select_demote_indices(importance: Optional[torch.Tensor], n_demote: int, hot
         dev = importance.device if importance is not None else None
         return torch.arange(n_demote, device=dev)
     nat.require_device(importance)
+    if not 0 <= n_demote <= hot_len:
+        raise ValueError(f"n_demote {n_demote} outside [0, {hot_len}]")
     protect_initial = 4
     protect_recent = min(16, hot_budget // 4)
-    scores = importance.to(torch.float32).clone()
-    scores[..., :protect_initial] = float("inf")
-    scores[..., max(0, hot_len - protect_recent):] = float("inf")
-    _, idx = scores.topk(n_demote, dim=-1, largest=False)
-    idx, _ = idx.sort(dim=-1)
+    scores = nat.dev_contig(importance, torch.float32)
+    rows = scores.numel() // hot_len if hot_len else 0
+    idx = torch.empty(importance.shape[:-1] + (n_demote,), dtype=torch.int64, device=importance.device)
+    lib = nat.load()
+    nat.check(lib.akv_select_demote(scores.data_ptr(), rows, hot_len, n_demote, protect_initial, protect_recent,
+                                    idx.data_ptr(), nat.stream_of(scores)), "select_demote_indices")
     return idx
 
 

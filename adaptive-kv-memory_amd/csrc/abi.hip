@@ -534,6 +534,20 @@ int akv_prefill_attn(const akv_prefill_args *a, void *stream) {
     return ok();
 }
 
+int akv_select_demote(const float *scores, int64_t rows, int64_t len, int64_t n_demote, int32_t protect_first,
+                      int32_t protect_last, int64_t *out, void *stream) {
+    if (rows < 0 || len < 0 || n_demote < 0) return fail(AKV_E_SHAPE, "negative size");
+    if (n_demote > len) return fail(AKV_E_SHAPE, "n_demote (%lld) > len (%lld)", (long long)n_demote, (long long)len);
+    if (protect_first < 0 || protect_last < 0) return fail(AKV_E_SHAPE, "negative protection");
+    if (rows == 0 || n_demote == 0) return ok();
+    if (!scores || !out) return fail(AKV_E_INVALID, "scores and out are required");
+    if (!aligned16(scores) || !aligned16(out)) return fail(AKV_E_ALIGN, "scores/out must be 16-byte aligned");
+    if (len >= ((int64_t)1 << 31)) return fail(AKV_E_SHAPE, "len too large");
+    hipError_t e = akv::select_launch(scores, rows, len, n_demote, protect_first, protect_last, out, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "select launch");
+    return ok();
+}
+
 int akv_importance_update(const akv_importance_args *a, void *stream) {
     if (!a) return fail(AKV_E_INVALID, "args is NULL");
     if (a->abi_version != AKV_ABI_VERSION) return fail(AKV_E_ABI, "ABI mismatch");

@@ -136,6 +136,109 @@ __global__ __launch_bounds__(256) void importance_kernel(const ImportanceParams 
     p.scores[n] = s;
 }
 
+// ------------------------------------------------------------ demote selection
+// One workgroup (1024 threads) per row.  Scores become order-preserving 32-bit
+// keys (-0 as +0, NaN above +inf, protected positions = +inf); a 4-pass radix
+// select (8 bits per pass, per-wave LDS histograms) finds the key tau of the
+// n-th smallest and how many tau-valued elements to take; a block-wide scan of
+// per-thread counts over contiguous chunks then writes the selected indices in
+// ascending order (equal keys: lowest index first).
+namespace {
+__device__ __forceinline__ uint32_t order_key(float f) {
+    uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0xFFFFFFFFu;  // NaN sorts after +inf
+    if (u == 0x80000000u) u = 0u;                             // -0 == +0
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+constexpr uint32_t kKeyInf = 0xFF800000u;  // order_key(+inf)
+}  // namespace
+
+__global__ __launch_bounds__(1024) void select_kernel(const float *scores, int64_t len, int64_t n, int64_t pf,
+                                                      int64_t pl, int64_t *out) {
+    __shared__ uint32_t hist[16][256];
+    __shared__ uint32_t tot[256];
+    __shared__ uint32_t cnt_lt[1024], cnt_eq[1024];
+    __shared__ uint32_t s_prefix, s_k;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const float *srow = scores + (int64_t)blockIdx.x * len;
+    int64_t *orow = out + (int64_t)blockIdx.x * n;
+    const int64_t rec = len - pl > 0 ? len - pl : 0;
+    auto key = [&](int64_t i) -> uint32_t { return (i < pf || i >= rec) ? kKeyInf : order_key(srow[i]); };
+    if (tid == 0) {
+        s_prefix = 0u;
+        s_k = (uint32_t)n;  // rank (1-based) of the key to find among the remaining candidates
+    }
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        for (int i = tid; i < 16 * 256; i += 1024) (&hist[0][0])[i] = 0u;
+        __syncthreads();
+        const uint32_t prefix = s_prefix;
+        const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
+        for (int64_t i = tid; i < len; i += 1024) {
+            const uint32_t k = key(i);
+            if ((k & hmask) == prefix) atomicAdd(&hist[wave][(k >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (tid < 256) {
+            uint32_t t = 0;
+#pragma unroll
+            for (int w = 0; w < 16; ++w) t += hist[w][tid];
+            tot[tid] = t;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t k = s_k, cum = 0;
+            int b = 0;
+            for (; b < 255; ++b) {
+                if (cum + tot[b] >= k) break;
+                cum += tot[b];
+            }
+            s_k = k - cum;
+            s_prefix = prefix | ((uint32_t)b << shift);
+        }
+        __syncthreads();
+    }
+    const uint32_t tau = s_prefix, take_eq = s_k;  // take the first take_eq elements equal to tau
+    // per-thread contiguous chunk counts, then exclusive scans
+    const int64_t chunk = (len + 1023) / 1024;
+    const int64_t c0 = (int64_t)tid * chunk, c1 = c0 + chunk < len ? c0 + chunk : len;
+    uint32_t lt = 0, eq = 0;
+    for (int64_t i = c0; i < c1; ++i) {
+        const uint32_t k = key(i);
+        lt += k < tau;
+        eq += k == tau;
+    }
+    cnt_lt[tid] = lt;
+    cnt_eq[tid] = eq;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {  // inclusive scans (Hillis-Steele)
+        const uint32_t a = tid >= off ? cnt_lt[tid - off] : 0u, e = tid >= off ? cnt_eq[tid - off] : 0u;
+        __syncthreads();
+        cnt_lt[tid] += a;
+        cnt_eq[tid] += e;
+        __syncthreads();
+    }
+    uint32_t lt_before = cnt_lt[tid] - lt, eq_before = cnt_eq[tid] - eq;
+    for (int64_t i = c0; i < c1; ++i) {
+        const uint32_t k = key(i);
+        if (k < tau) {
+            const uint32_t pos = lt_before + (eq_before < take_eq ? eq_before : take_eq);
+            orow[pos] = i;
+            ++lt_before;
+        } else if (k == tau) {
+            if (eq_before < take_eq) orow[lt_before + eq_before] = i;
+            ++eq_before;
+        }
+    }
+}
+
+hipError_t select_launch(const float *scores, int64_t rows, int64_t len, int64_t n, int64_t pf, int64_t pl,
+                         int64_t *out, hipStream_t s) {
+    if (rows <= 0 || n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(1024), 0, s, scores, len, n, pf, pl, out);
+    return hipGetLastError();
+}
+
 hipError_t dequant_launch(const DequantParams &p, hipStream_t s) {
     const int64_t tasks = (int64_t)p.nbh * p.n_warm * (p.D / 8);
     if (tasks == 0) return hipSuccess;

@@ -245,6 +245,15 @@ int64_t akv_prefill_workspace_bytes(const akv_prefill_args *args);
  * (akv/triton_ops.py:466-515), which dequantize the whole warm tier first. */
 int akv_prefill_attn(const akv_prefill_args *args, void *stream);
 
+/* ------------------------------------------------------- demote selection */
+
+/* AKVLayer._select_demote_indices (akv/drop_in.py:392-413) on the device: for each of `rows`
+ * rows of `len` fp32 importance scores, the indices of the n_demote smallest after positions
+ * [0, protect_first) and [max(0, len - protect_last), len) are set to +inf; written ascending to
+ * out [rows][n_demote] i64.  Equal scores take the lower index first (NaN sorts above +inf). */
+int akv_select_demote(const float *scores, int64_t rows, int64_t len, int64_t n_demote,
+                      int32_t protect_first, int32_t protect_last, int64_t *out, void *stream);
+
 /* --------------------------------------------------------------- misc */
 
 int akv_abi_version(void);
