@@ -219,8 +219,13 @@ def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def workspace(nbytes: int, device) -> torch.Tensor:
-    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+def workspace(nbytes: int, device, zero: bool = False) -> torch.Tensor:
+    """Device scratch for one call.  Decode workspaces start zeroed: their split
+    arrival counters must read zero before the first call (each call leaves them so)."""
+    n = max(int(nbytes), 256)
+    if zero:
+        return torch.zeros(n, dtype=torch.uint8, device=device)
+    return torch.empty(n, dtype=torch.uint8, device=device)
 
 
 def default_sm_scale(d: int) -> float:

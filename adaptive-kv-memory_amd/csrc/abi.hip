@@ -39,7 +39,8 @@ int64_t align256(int64_t x) { return round_up(x, 256); }
 struct Plan {
     int nchunk, prows, n_wsplit, n_hsplit, nsplit;
     int64_t wsplit_len, hsplit_len, N;
-    int64_t part_bytes, rowstat_bytes, flag_bytes, stash_bytes, total;
+    int64_t ctr_bytes, part_bytes, rowstat_bytes, flag_bytes, stash_bytes, total;
+    bool fused;  // the fast split kernel merges its own splits (arrival counters at offset 0)
 };
 
 constexpr int kWaves = 4;
@@ -50,6 +51,9 @@ constexpr int kWaves = 4;
 // least one unit per wave.  Without an explicit count the schedule aims at a
 // few workgroups per compute unit of the 256-CU MI355X.
 constexpr int kCUs = 256;
+// Largest split count the fast kernel merges itself (its last workgroup reads
+// every partial of a row chunk); larger counts use decode_reduce_kernel.
+constexpr int kFusedMaxSplits = 32;
 
 bool fast_path(const akv_decode_args *a) {
     const akv_warm_desc &w = a->warm;
@@ -116,12 +120,14 @@ void make_plan(const akv_decode_args *a, Plan *pl) {
     pl->n_hsplit = nh > 0 ? (int)((nh + pl->hsplit_len - 1) / pl->hsplit_len) : 0;
     pl->nsplit = pl->n_wsplit + pl->n_hsplit;
     }
+    pl->fused = fast && pl->nsplit <= kFusedMaxSplits;
+    pl->ctr_bytes = align256(pairs * 8);
     pl->part_bytes = align256(pairs * pl->nsplit * (int64_t)pl->prows * (a->D + 4) * 4);
     pl->rowstat_bytes = align256((int64_t)a->B * a->Hq * a->M * 2 * 4);
     pl->flag_bytes = 256;
     const bool need_stash = a->attn_weights == nullptr && a->scores != nullptr;
     pl->stash_bytes = need_stash ? align256((int64_t)a->B * a->Hq * a->M * pl->N * 4) : 0;
-    pl->total = pl->part_bytes + pl->rowstat_bytes + pl->flag_bytes + pl->stash_bytes;
+    pl->total = pl->ctr_bytes + pl->part_bytes + pl->rowstat_bytes + pl->flag_bytes + pl->stash_bytes;
 }
 
 int check_decode(const akv_decode_args *a) {
@@ -294,6 +300,8 @@ int akv_decode_attn(const akv_decode_args *a, void *stream) {
     int sym_src[2] = {0, 0};
     const int *sym_ptr = nullptr;
     char *ws = (char *)a->workspace;
+    if (pl.fused) p.split_ctr = (uint64_t *)ws;
+    ws += pl.ctr_bytes;
     p.part = (float *)ws;
     p.rowstats = (float *)(ws + pl.part_bytes);
     int *flags = (int *)(ws + pl.part_bytes + pl.rowstat_bytes);

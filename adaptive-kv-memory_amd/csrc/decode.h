@@ -37,6 +37,8 @@ struct DecodeParams {
     int64_t wsplit_len, hsplit_len;
     // outputs / workspace
     float *part;                  // split partials
+    uint64_t *split_ctr;          // fast kernel: arrival counts per (b, kv-head, row chunk), a byte per XCD; null = merge
+                                  // in decode_reduce_kernel / finish_kernel
     float *stash;                 // [B][Hq][M][N] log2-domain logits (or null)
     float *rowstats;              // [B*Hq*M][2] (M, L)
     _Float16 *out;                // [B][Hq][M][D]

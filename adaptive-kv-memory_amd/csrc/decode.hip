@@ -860,13 +860,20 @@ __global__ __launch_bounds__(256) void finish_kernel(const DecodeParams p) {
     const int64_t PS = D + 4;
     const int64_t pstride = (int64_t)p.prows * PS;
 
-    // output merge of one (chunk, row)
-    const int n_merge = p.B * p.Hkv * p.nchunk * p.prows;
+    // output merge of one (chunk, row), unless the split kernel merged its own splits
+    const int n_merge = p.split_ctr ? 0 : p.B * p.Hkv * p.nchunk * p.prows;
     if ((int)blockIdx.x < n_merge)
         merge_split_row<D>(p, blockIdx.x / p.prows, blockIdx.x % p.prows, sm, sls, accl);
 
-    // statistics of every row, one thread per row with all its split loads in flight
-    for (int r = tid; r < rows; r += 256) {
+    // statistics of every row: from the split kernel's merge, or one thread per
+    // row with all its split loads in flight
+    if (p.split_ctr) {
+        for (int r = tid; r < rows; r += 256) {
+            rM[r] = p.rowstats[2 * r];
+            rW[r] = 1.0f / p.rowstats[2 * r + 1];
+        }
+    }
+    for (int r = tid; r < rows && !p.split_ctr; r += 256) {
         const int b = r / (p.Hq * p.M), hm = r % (p.Hq * p.M);
         const int h = hm / p.M, m = hm % p.M;
         const int kvh = h / p.g, rk = (h % p.g) * p.M + m;  // row within the kv-head's g*M rows
@@ -1013,20 +1020,21 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
         e = legacy_sym_launch(p.kz, p.vz, (int64_t)sym_src_dt_n[1], sym_src_dt_n[0], (int *)p.sym_flags, s);
         if (e != hipSuccess) return e;
     }
+    if (p.split_ctr && !decode_fast_eligible(p, wk)) return hipErrorInvalidValue;  // only the fast kernel merges
     if (decode_fast_eligible(p, wk)) e = decode_fast_split_launch(p, kb, vb, s);
     else e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M;
     if (p.stash && rows <= kFinishRows) {
-        // one launch: output merge + weights / importance
+        // one launch: output merge (unless the split kernel did it) + weights / importance
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
-        const int64_t n_tok = (nmax + 63) / 64, n_merge = (int64_t)p.B * p.Hkv * p.nchunk * p.prows;
+        const int64_t n_tok = (nmax + 63) / 64, n_merge = p.split_ctr ? 0 : (int64_t)p.B * p.Hkv * p.nchunk * p.prows;
         const unsigned nwg = (unsigned)(n_tok > n_merge ? n_tok : n_merge);
         if (p.D == 64) hipLaunchKernelGGL(finish_kernel<64>, dim3(nwg), dim3(256), 0, s, p);
         else hipLaunchKernelGGL(finish_kernel<128>, dim3(nwg), dim3(256), 0, s, p);
         return hipGetLastError();
     }
-    if ((e = decode_reduce_launch(p, s)) != hipSuccess) return e;
+    if (!p.split_ctr && (e = decode_reduce_launch(p, s)) != hipSuccess) return e;
     if (p.stash) {
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
         hipLaunchKernelGGL(weights_importance_kernel, dim3((unsigned)((nmax + 63) / 64)), dim3(256), 0, s, p);

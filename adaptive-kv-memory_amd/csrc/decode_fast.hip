@@ -51,12 +51,21 @@ namespace akv {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kWaves = 12;           // waves per workgroup (one workgroup per CU, 3 per SIMD)
-constexpr int kUnit = 32;            // warm tokens per ring slot
-constexpr int kNS = 2;               // ring slots per wave (deeper rings only lengthen the tail)
+#ifndef AKV_FAST_WAVES
+#define AKV_FAST_WAVES 12
+#endif
+#ifndef AKV_FAST_NS
+#define AKV_FAST_NS 2
+#endif
+constexpr int kWaves = AKV_FAST_WAVES;  // waves per workgroup (one workgroup per CU, 3 per SIMD)
+constexpr int kUnit = 32;               // warm tokens per ring slot
+constexpr int kNS = AKV_FAST_NS;        // ring slots per wave (deeper rings only lengthen the tail)
 constexpr int kLdsCap = 160 * 1024;  // LDS of one CU
 constexpr int kKmetaBytes = 3 * 4 * 16 * 4;  // [s | n | z][group][pair] u32
 constexpr int kHotLoads = 4;         // 16 tokens x 256 B = 4 KiB = 4 wave loads
+constexpr int kQldsBytes = 4 * 64 * 16;  // Q operand of the workgroup
+constexpr int kAccRow = kD + 4;      // fp32 row of the end-of-split merge in LDS (the pad spreads a
+                                     // wave's 64 row/chunk writes over the banks)
 template <int BK, int BV, int NG>
 struct WarmLayout {
     static constexpr int KR = 16 * BK, VR = 16 * BV;  // packed row bytes (D = 128)
@@ -106,6 +115,40 @@ __device__ __forceinline__ void stash4(const DecodeParams &p, int64_t strow, int
         if (i < nvalid) dst[i] = s[i] * sl2;
 }
 
+// Online merge of the nsplit partials (m, l, acc) of row rr, channels 4 c4 .. +3,
+// loaded with cache policy CP.
+template <int CP>
+__device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t prs, int nsplit, int64_t pstride, int rr, int c4,
+                                               float &M, float &L, f4 &a) {
+    constexpr int PS = 128 + 4, KS = 16;  // partial row; splits per batch of loads
+    for (int s0 = 0; s0 < nsplit; s0 += KS) {
+        f2 ml[KS];
+        f4 xs[KS];
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const int off = (int)(((s0 + k) * pstride + rr * PS) * 4);
+            const bool in = s0 + k < nsplit;
+            ml[k] = in ? __builtin_bit_cast(f2, __builtin_amdgcn_raw_buffer_load_b64(prs, off, 0, CP)) : (f2){-INFINITY, 0.f};
+            xs[k] = in ? __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(prs, off + 16 + 16 * c4, 0, CP))
+                       : (f4){0.f, 0.f, 0.f, 0.f};
+        }
+        float nm = M;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) nm = fmaxf(nm, ml[k][0]);
+        if (nm == -INFINITY) continue;
+        const float fo = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(M - nm);
+        a *= fo;
+        L *= fo;
+#pragma unroll
+        for (int k = 0; k < KS; ++k) {
+            const float f = (ml[k][0] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ml[k][0] - nm);
+            a += f * xs[k];
+            L += f * ml[k][1];
+        }
+        M = nm;
+    }
+}
+
 }  // namespace
 
 
@@ -113,24 +156,27 @@ __device__ __forceinline__ void stash4(const DecodeParams &p, int64_t strow, int
 constexpr int kNone = 0, kWarm = 1, kHotK = 2, kHotV = 3;
 
 #ifndef AKV_FAST_WAVES_PER_EU
-#define AKV_FAST_WAVES_PER_EU 3
+#define AKV_FAST_WAVES_PER_EU (AKV_FAST_WAVES / 4)
 #endif
 // Loads still in flight behind the oldest ring slot, given how many of the
-// younger slots hold a warm unit (nw) or a hot half (nh); nw + nh <= 2.
-template <int NLW, int NLH>
+// younger slots hold a warm unit (nw) or a hot half (nh); nw + nh <= MAXY.
+template <int NLW, int NLH, int MAXY, int W = 0, int H = 0>
 __device__ __forceinline__ void wait_younger(int nw, int nh) {
-    if (nw == 2) wait_vm<2 * NLW>();
-    else if (nw == 1 && nh == 1) wait_vm<NLW + NLH>();
-    else if (nw == 1) wait_vm<NLW>();
-    else if (nh == 2) wait_vm<2 * NLH>();
-    else if (nh == 1) wait_vm<NLH>();
+    if constexpr (W + H <= MAXY) {
+        if (nw == W && nh == H) {
+            wait_vm<W * NLW + H * NLH>();
+            return;
+        }
+    }
+    if constexpr (H < MAXY) wait_younger<NLW, NLH, MAXY, W, H + 1>(nw, nh);
+    else if constexpr (W < MAXY) wait_younger<NLW, NLH, MAXY, W + 1, 0>(nw, nh);
     else wait_vm<0>();
 }
 
 template <int BK, int BV, int NG, int NS>
 __global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(AKV_FAST_WAVES_PER_EU, AKV_FAST_WAVES_PER_EU)))
 void decode_fast_kernel(const DecodeParams p) {
-    static_assert(NS == 2 || NS == 3, "ring depth");
+    static_assert(NS >= 2 && NS <= 4, "ring depth");
     using L = WarmLayout<BK, BV, NG>;
     constexpr int KSTEPS = kD / 32;
     constexpr int NLW = L::NLOAD;     // loads of a warm unit
@@ -141,14 +187,26 @@ void decode_fast_kernel(const DecodeParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int col = lane & 15, grp = lane >> 4;
-    const int split = blockIdx.x, kvh = blockIdx.y;
-    const int b = blockIdx.z / p.nchunk, chunk = blockIdx.z % p.nchunk;
+    // Workgroup -> (split, kv-head, batch x row chunk).  Workgroups are handed to
+    // the 8 XCDs round-robin by linear id; the order below gives each XCD a
+    // contiguous run of (pair, split) items, so all splits of a pair usually share
+    // one L2 and the in-kernel split merge reads their partials from it.
+    int wid = (int)blockIdx.x;
+    {
+        const int nwg = (int)gridDim.x;
+        if (nwg % 8 == 0) wid = (wid % 8) * (nwg / 8) + wid / 8;
+    }
+    const int split = wid % p.nsplit, kvh = (wid / p.nsplit) % p.Hkv;
+    const int bz = wid / (p.nsplit * p.Hkv);
+    const int b = bz / p.nchunk, chunk = bz % p.nchunk;
     const int row0 = chunk * 16;
     const int nrows = min(16, p.R - row0);
     const int slot_bytes = p.slot_bytes;
     unsigned char *ring = smem + wave * (NS * slot_bytes + kKmetaBytes);
     unsigned char *kmeta = ring + NS * slot_bytes;
     unsigned *work = (unsigned *)(smem + kWaves * (NS * slot_bytes + kKmetaBytes));  // item counter
+    // Q operand of the QK MFMAs, [step][lane] x 16 B, shared by the waves
+    u4 *qlds = (u4 *)(smem + kWaves * (NS * slot_bytes + kKmetaBytes) + 16);
 
     const int r = row0 + col;
     const int row_valid = col < nrows;
@@ -160,16 +218,16 @@ void decode_fast_kernel(const DecodeParams p) {
     const int64_t warm_base = p.hot_first ? p.n_hot : 0;  // logical position of warm token 0
     const int64_t hot_base = p.hot_first ? 0 : p.n_warm;
 
-    // this workgroup's items: hot 16-token tiles, then warm 32-token units
+    // this workgroup's items: warm 32-token units, then hot 16-token tiles (the
+    // cheap hot items come last and even out the waves' finishing times)
     const int nw = (int)p.n_warm, nh = (int)p.n_hot;
     const int w_begin = min(split * (int)p.wsplit_len, nw), w_end = min(w_begin + (int)p.wsplit_len, nw);
     const int h_begin = min(split * (int)p.hsplit_len, nh), h_end = min(h_begin + (int)p.hsplit_len, nh);
-    const int u_first = w_begin / kUnit, n_wu = (w_end + kUnit - 1) / kUnit - u_first;
-    const int t_first = h_begin / 16, n_ht = (h_end + 15) / 16 - t_first;
-    const int n_items = (h_end > h_begin ? n_ht : 0) + (w_end > w_begin ? n_wu : 0);
-    const int n_hot_items = h_end > h_begin ? n_ht : 0;
-    if (threadIdx.x == 0) *work = 0u;
-    __syncthreads();  // item counter initialised before any wave takes an item
+    const int u_first = w_begin / kUnit, n_wu = w_end > w_begin ? (w_end + kUnit - 1) / kUnit - u_first : 0;
+    const int t_first = h_begin / 16, n_ht = h_end > h_begin ? (h_end + 15) / 16 - t_first : 0;
+    const int n_items = n_wu + n_ht;
+    // items 0 .. kWaves-1 go to waves 0 .. kWaves-1; the counter hands out the rest
+    if (threadIdx.x == 0) *work = (unsigned)kWaves;
 
     WarmRes R;
     {
@@ -186,7 +244,8 @@ void decode_fast_kernel(const DecodeParams p) {
 
     // ---- the ring: a queue of NS slots, oldest first; a hot item is two units (K, then V)
     int qk[NS], qi[NS];
-    int pend = -1;  // hot tile whose V half is still to be issued
+    int pend = -1;         // hot tile whose V half is still to be issued
+    bool claimed = false;  // the first item is the wave's own; later ones come from the counter
     auto next_unit = [&](int &k, int &id) {
         if (pend >= 0) {
             k = kHotV;
@@ -194,19 +253,22 @@ void decode_fast_kernel(const DecodeParams p) {
             pend = -1;
             return;
         }
-        unsigned it = 0;
-        if (lane == 0) it = atomicAdd(work, 1u);
-        it = __builtin_amdgcn_readfirstlane(it);
+        unsigned it = (unsigned)wave;
+        if (claimed) {
+            if (lane == 0) it = atomicAdd(work, 1u);
+            it = __builtin_amdgcn_readfirstlane(it);
+        }
+        claimed = true;
         if ((int)it >= n_items) {
             k = kNone;
             id = 0;
-        } else if ((int)it < n_hot_items) {
-            k = kHotK;
-            id = t_first + (int)it;
-            pend = id;
-        } else {
+        } else if ((int)it < n_wu) {
             k = kWarm;
-            id = u_first + (int)it - n_hot_items;
+            id = u_first + (int)it;
+        } else {
+            k = kHotK;
+            id = t_first + (int)it - n_wu;
+            pend = id;
         }
     };
     auto issue = [&](int k, int id, unsigned char *slot) {
@@ -214,19 +276,10 @@ void decode_fast_kernel(const DecodeParams p) {
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
-    // Only the first slot is filled up front: every wave's first unit is in
-    // the memory queue before any wave's second, so compute starts as soon as
-    // a first unit lands; the other slots fill once it has (loop, first pass).
-    next_unit(qk[0], qi[0]);
-    issue(qk[0], qi[0], ring);
-#pragma unroll
-    for (int s2 = 1; s2 < NS; ++s2) qk[s2] = kNone;
-    bool primed = false;
-
     // Q operand (B of QK): lane = (row col, channel group grp), in the channel
-    // order the warm code pairs come out in (hot K is permuted to match)
-    h8 qop[KSTEPS];
-    {
+    // order the warm code pairs come out in (hot K is permuted to match).  Wave 0
+    // stages it in LDS for the workgroup before it takes its first unit.
+    if (wave == 0) {
         const u4 *qrow = (const u4 *)(p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp);
         uint32_t nat[16], pairs[16];
 #pragma unroll
@@ -241,9 +294,18 @@ void decode_fast_kernel(const DecodeParams p) {
         hot_k_pairs<BK>(nat, pairs);
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st)
-            qop[st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
+            qlds[st * 64 + lane] = (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]};
     }
-
+    // Only the first slot is filled up front: every wave's first unit is in
+    // the memory queue before any wave's second, so compute starts as soon as
+    // a first unit lands; the other slots fill once it has (loop, first pass).
+    next_unit(qk[0], qi[0]);
+    issue(qk[0], qi[0], ring);
+#pragma unroll
+    for (int s2 = 1; s2 < NS; ++s2) qk[s2] = kNone;
+    bool primed = false;
+    __syncthreads();  // Q operand and item counter in LDS before any wave uses them
+    auto qop = [&](int st) { return __builtin_bit_cast(h8, qlds[st * 64 + lane]); };
 
     Soft stt;
     stt.m2 = -INFINITY;
@@ -281,7 +343,7 @@ void decode_fast_kernel(const DecodeParams p) {
                 nwy += qk[i] == kWarm;
                 nhy += qk[i] == kHotK || qk[i] == kHotV;
             }
-            wait_younger<NLW, NLH>(nwy, nhy);
+            wait_younger<NLW, NLH, NS - 1>(nwy, nhy);
         }
         if (!primed) {
             primed = true;
@@ -293,10 +355,10 @@ void decode_fast_kernel(const DecodeParams p) {
         }
 
         if (k == kWarm) {
-            // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS;
-            //      the fast paths hold when no -1024 s overflows (K and V scales of the unit)
+            // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS
+            //      and read back per MFMA step; the fast paths hold when no -1024 s overflows
+            //      (K and V scales of the unit)
             bool kfast, vfast;
-            h2 ksc[16], kng[16], kze[16];
             {
                 const h2 s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
                 const h2 z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
@@ -315,138 +377,150 @@ void decode_fast_kernel(const DecodeParams p) {
                 kmw[(1 * 4 + g2) * 16 + pi2] = nb;
                 kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
                 __builtin_amdgcn_wave_barrier();
-                const u4 *src = (const u4 *)kmeta;
-#pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    const u4 av = src[(0 * 4 + grp) * 4 + q4];
-                    const u4 nv = src[(1 * 4 + grp) * 4 + q4];
-                    const u4 zv = src[(2 * 4 + grp) * 4 + q4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const uint32_t ae = av[e], ne = nv[e], ze = zv[e];
-                        ksc[4 * q4 + e] = as_h2(ae);
-                        kng[4 * q4 + e] = as_h2(ne);
-                        kze[4 * q4 + e] = as_h2(ze);
-                    }
-                }
             }
+            const u4 *kmr = (const u4 *)kmeta;
 
             const int tok0 = id * kUnit;  // first token of the unit (pair-local warm index)
-            // ---- phase 1: QK of both tiles (the K meta dies after it)
-            f4 sc[2];
+            // ---- QK of both 16-token halves, step by step (two independent MFMA chains)
+            KWin<BK> W[2];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 uint32_t kraw[BK];
-                {
-                    const uint32_t *kp = (const uint32_t *)(slot + k_lane + 16 * h * L::KR);
+                const uint32_t *kp = (const uint32_t *)(slot + k_lane + 16 * h * L::KR);
 #pragma unroll
-                    for (int jj = 0; jj < BK; ++jj) kraw[jj] = kp[jj];
-                }
-                KWin<BK> W;
-                k_windows<BK>(kraw, W);
-                sc[h] = (f4){0.f, 0.f, 0.f, 0.f};
-                if (kfast) {
+                for (int jj = 0; jj < BK; ++jj) kraw[jj] = kp[jj];
+                k_windows<BK>(kraw, W[h]);
+            }
+            f4 sc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            if (kfast) {
 #pragma unroll
-                    for (int st = 0; st < KSTEPS; ++st) {
+                for (int st = 0; st < KSTEPS; ++st) {
+                    const u4 av = kmr[(0 * 4 + grp) * 4 + st], nv = kmr[(1 * 4 + grp) * 4 + st];
+                    const u4 zv = kmr[(2 * 4 + grp) * 4 + st];
+                    const h8 qst = qop(st);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
                         h8 a;
 #pragma unroll
                         for (int kk = 0; kk < 4; ++kk) {
                             const int pi = 4 * st + kk;
-                            const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
-                            h2 v = pk_fma(as_h2(uu), ksc[pi], kng[pi]);
-                            v = v + kze[pi];
+                            const uint32_t uu = (k_window_of<BK>(W[h], pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            h2 v = pk_fma(as_h2(uu), as_h2(av[kk]), as_h2(nv[kk]));
+                            v = v + as_h2(zv[kk]);
                             a[2 * kk] = v[0];
                             a[2 * kk + 1] = v[1];
                         }
-                        sc[h] = mfma_k32(a, qop[st], sc[h]);
+                        sc[h] = mfma_k32(a, qst, sc[h]);
                     }
-                } else {
+                }
+            } else {
 #pragma unroll
-                    for (int st = 0; st < KSTEPS; ++st) {
+                for (int st = 0; st < KSTEPS; ++st) {
+                    const u4 av = kmr[(0 * 4 + grp) * 4 + st], zv = kmr[(2 * 4 + grp) * 4 + st];
+                    const h8 qst = qop(st);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
                         h8 a;
 #pragma unroll
                         for (int kk = 0; kk < 4; ++kk) {
                             const int pi = 4 * st + kk;
-                            const uint32_t uu = (k_window_of<BK>(W, pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            const uint32_t uu = (k_window_of<BK>(W[h], pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
                             const _Float16 mv = (_Float16)magic_val(koff<BK>(pi));
                             const h2 c = as_h2(uu) - (h2){mv, mv};  // the code, exactly
-                            h2 v = c * ksc[pi];
-                            v = v + kze[pi];
+                            h2 v = c * as_h2(av[kk]);
+                            v = v + as_h2(zv[kk]);
                             a[2 * kk] = v[0];
                             a[2 * kk + 1] = v[1];
                         }
-                        sc[h] = mfma_k32(a, qop[st], sc[h]);
+                        sc[h] = mfma_k32(a, qst, sc[h]);
                     }
                 }
             }
 
-            // ---- phase 2, per tile: V dequant, softmax, PV
+            // ---- softmax over the 32 tokens (ragged tail masked; logits stashed)
+            if (tok0 + kUnit > nw) {
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint32_t vraw[4];
+                for (int h = 0; h < 2; ++h) {
+                    const int nvalid = min(4, nw - (tok0 + 16 * h + 4 * grp));
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii)
+                        if (ii >= nvalid) sc[h][ii] = -INFINITY;
+                }
+            }
+            if (p.stash) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int t0 = tok0 + 16 * h;
+                    stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], sl2, min(4, nw - (t0 + 4 * grp)));
+                }
+            }
+            const h8 pop = softmax32(stt, sc[0], sc[1], sl2);
+
+            // ---- V: lane (chunk col, tokens 4 grp .. +3 of each half); token pairs per dword
+            uint32_t vraw[2][4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int ii = 0; ii < 4; ++ii) {
                     const unsigned char *vp = slot + v_lane + (16 * h + ii) * L::VR;
                     if (BV == 3) {  // the chunk's 3 bytes from the aligned 8 around them
                         const uint32_t *vq = (const uint32_t *)(slot + (v_lane & ~3) + (16 * h + ii) * L::VR);
-                        vraw[ii] = __builtin_amdgcn_alignbyte(vq[1], vq[0], v_lane & 3);
-                    } else vraw[ii] = BV == 2 ? lds_u16(vp) : *(const uint32_t *)vp;
+                        vraw[h][ii] = __builtin_amdgcn_alignbyte(vq[1], vq[0], v_lane & 3);
+                    } else vraw[h][ii] = BV == 2 ? lds_u16(vp) : *(const uint32_t *)vp;
                 }
-                h2 vs[2], vz[2];
+            h2 vs[2][2], vz[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int pp = 0; pp < 2; ++pp) {
                     const int ta = 16 * h + 2 * pp;  // + 4 grp (in vm_lane)
-                    vs[pp] = lds_h2(slot + L::VS + vm_lane + ta * NG * 2, slot + L::VS + vm_lane + (ta + 1) * NG * 2);
-                    vz[pp] = lds_h2(slot + L::VZ + vm_lane + ta * NG * 2, slot + L::VZ + vm_lane + (ta + 1) * NG * 2);
+                    vs[h][pp] = lds_h2(slot + L::VS + vm_lane + ta * NG * 2, slot + L::VS + vm_lane + (ta + 1) * NG * 2);
+                    vz[h][pp] = lds_h2(slot + L::VZ + vm_lane + ta * NG * 2, slot + L::VZ + vm_lane + (ta + 1) * NG * 2);
                 }
-                uint32_t vpair[2][8];
+            uint32_t win[2][2][VSlot<BV>::NW];
 #pragma unroll
-                for (int pp = 0; pp < 2; ++pp) {
-                    uint32_t win[VSlot<BV>::NW];
-                    v_windows<BV>(vraw[2 * pp], vraw[2 * pp + 1], win);
-                    if (vfast) {
-                        h2 vn[v_noffs<BV>()];
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) v_windows<BV>(vraw[h][2 * pp], vraw[h][2 * pp + 1], win[h][pp]);
+            if (vfast) {
+                h2 vn[2][2][v_noffs<BV>()];
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
                         for (int oi = 0; oi < v_noffs<BV>(); ++oi) {
                             const _Float16 m = (_Float16)(-magic_val(oi * v_ostep<BV>()));
-                            vn[oi] = vs[pp] * (h2){m, m};
+                            vn[h][pp][oi] = vs[h][pp] * (h2){m, m};
                         }
 #pragma unroll
-                        for (int kk = 0; kk < 8; ++kk) {
-                            const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
-                            h2 v = pk_fma(as_h2(uu), vs[pp], vn[voff<BV>(kk) / v_ostep<BV>()]);
-                            vpair[pp][kk] = as_u32(v);
-                        }
-                    } else {
+                for (int kk = 0; kk < 8; ++kk) {
+                    uint32_t d[4];
 #pragma unroll
-                        for (int kk = 0; kk < 8; ++kk) {
-                            const uint32_t uu = (win[vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
-                            const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
-                            const h2 c = as_h2(uu) - (h2){mv, mv};
-                            h2 v = c * vs[pp];
-                            vpair[pp][kk] = as_u32(v);
-                        }
+                    for (int q = 0; q < 4; ++q) {
+                        const int h = q >> 1, pp = q & 1;
+                        const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                        d[q] = as_u32(pk_fma(as_h2(uu), vs[h][pp], vn[h][pp][voff<BV>(kk) / v_ostep<BV>()]));
                     }
+                    stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
                 }
-
-                // ---- softmax
-                f4 sh = sc[h];
-                const int t0 = tok0 + 16 * h;
-                const int nvalid = min(4, nw - (t0 + 4 * grp));
-                if (t0 + 16 > nw) {
+            } else {
 #pragma unroll
-                    for (int ii = 0; ii < 4; ++ii)
-                        if (ii >= nvalid) sh[ii] = -INFINITY;
+                for (int kk = 0; kk < 8; ++kk) {
+                    uint32_t d[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int h = q >> 1, pp = q & 1;
+                        const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                        const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
+                        const h2 c = as_h2(uu) - (h2){mv, mv};
+                        d[q] = as_u32(c * vs[h][pp]);
+                    }
+                    stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
                 }
-                stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sh, sl2, nvalid);
-                const h4 pop = softmax16(stt, sh, sl2);
-
-                // ---- PV
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk)
-                    stt.acc[kk] = mfma_k16(__builtin_bit_cast(h4, (u2){vpair[0][kk], vpair[1][kk]}), pop, stt.acc[kk]);
-                stt.accz = mfma_k16(__builtin_bit_cast(h4, (u2){as_u32(vz[0]), as_u32(vz[1])}), pop, stt.accz);
             }
+            stt.accz = mfma_k32(__builtin_bit_cast(h8, (u4){as_u32(vz[0][0]), as_u32(vz[0][1]), as_u32(vz[1][0]), as_u32(vz[1][1])}),
+                                pop, stt.accz);
         } else if (k == kHotK) {
             // ---- hot K tile: 16 tokens x 256 B; lane = (token col, 32 channels of group grp)
             uint32_t nat[16], pairs[16];
@@ -464,7 +538,7 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
             for (int st = 0; st < KSTEPS; ++st)
                 sh = mfma_k32(__builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]}),
-                              qop[st], sh);
+                              qop(st), sh);
             const int t0 = id * 16;
             const int nvalid = min(4, nh - (t0 + 4 * grp));
             if (t0 + 16 > nh) {
@@ -501,40 +575,103 @@ void decode_fast_kernel(const DecodeParams p) {
         head = head + 1 == NS ? 0 : head + 1;
     }
 
-    // ---- merge the waves (the ring memory is reused)
+    // ---- merge the waves (the ring memory is reused): every wave rescales its
+    //      rows to the workgroup maximum, then the 12 states are summed
     wait_vm<0>();
     stt.l = wsum16(stt.l);
     __syncthreads();
-    float *mlds = (float *)smem;                   // [W][16]
-    float *llds = mlds + kWaves * 16;              // [W][16]
-    float *alds = llds + kWaves * 16;              // [W][16][D]
-    if (grp == 0) {
-        mlds[wave * 16 + col] = stt.m2;
-        llds[wave * 16 + col] = stt.l;
-    }
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) alds[(wave * 16 + col) * kD + 8 * (4 * grp + ii) + kk] = stt.acc[kk][ii] + stt.accz[ii];
+    float *mlds = (float *)smem;                   // [W][16] running maxima
+    float *llds = mlds + kWaves * 16;              // [W][16] rescaled sums
+    float *alds = llds + kWaves * 16;              // [W][16][kAccRow] rescaled accumulators
+    if (grp == 0) mlds[wave * 16 + col] = stt.m2;
     __syncthreads();
-    float *part = p.part + ((bh * p.nchunk + chunk) * p.nsplit + split) * (int64_t)(p.prows * (kD + 4));
-    for (int e = threadIdx.x; e < nrows * kD; e += 64 * kWaves) {
-        const int rr = e / kD, ch = e % kD;
+    {
         float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, mlds[w * 16 + rr]);
-        float a = 0.f, l = 0.f;
+        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, mlds[w * 16 + col]);
+        const float fw = (stt.m2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(stt.m2 - mx);
+        if (grp == 0) llds[wave * 16 + col] = stt.l * fw;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
-            const float mw = mlds[w * 16 + rr];
-            const float f = (mw == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(mw - mx);
-            a += f * alds[(w * 16 + rr) * kD + ch];
-            l += f * llds[w * 16 + rr];
+        for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii)
+                alds[(wave * 16 + col) * kAccRow + 8 * (4 * grp + ii) + kk] = (stt.acc[kk][ii] + stt.accz[ii]) * fw;
+    }
+    __syncthreads();
+    const int64_t bhc = bh * p.nchunk + chunk;
+    constexpr int PS = kD + 4;  // partial row: (m, l, pad, pad, acc[D])
+    const int64_t pstride = (int64_t)p.prows * PS;
+    float *part = p.part + (bhc * p.nsplit + split) * pstride;
+    const bool fused = p.split_ctr != nullptr;
+    // this (batch, kv-head, row chunk)'s partials as a buffer; the fused merge
+    // moves them with write-through stores and coherent loads (cache policy sc1)
+    const __amdgpu_buffer_rsrc_t prs = make_rsrc(p.part + bhc * p.nsplit * pstride, (uint32_t)(p.nsplit * pstride * 4));
+    constexpr int kSc1 = 16;  // cache-policy bit sc1: coherent at device scope
+    const int tid = threadIdx.x;
+    if (tid < nrows * (kD / 4)) {  // thread = (row, channel quad); 512 <= 64 * kWaves
+        const int rr = tid / (kD / 4), c4 = tid % (kD / 4);
+        f4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) a += *(const f4 *)(alds + (w * 16 + rr) * kAccRow + 4 * c4);
+        const int off = (int)((split * pstride + rr * PS) * 4);
+        if (fused) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), prs, off + 16 + 16 * c4, 0, kSc1);
+        else *(f4 *)(part + rr * PS + 4 + 4 * c4) = a;
+        if (c4 == 0) {
+            float mx = -INFINITY, l = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                mx = fmaxf(mx, mlds[w * 16 + rr]);
+                l += llds[w * 16 + rr];
+            }
+            if (fused) __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2, (f2){mx, l}), prs, off, 0, kSc1);
+            else {
+                part[rr * PS + 0] = mx;
+                part[rr * PS + 1] = l;
+            }
         }
-        part[rr * (kD + 4) + 4 + ch] = a;
-        if (ch == 0) {
-            part[rr * (kD + 4) + 0] = mx;
-            part[rr * (kD + 4) + 1] = l;
+    }
+    if (!fused) return;
+
+    // ---- split merge in the kernel: the workgroup whose partial completes the
+    //      (batch, kv-head, row chunk) merges all of them.  The partials were
+    //      written through to the device coherence point (and the writer's L2);
+    //      waiting for the stores before the counter increment orders them before
+    //      it.  The merge reads them from its own L2 when every partial came from
+    //      its XCD, else from the coherence point.  The counter returns to zero.
+    wait_vm<0>();
+    __syncthreads();
+    if (tid == 0) {
+        // one byte per XCD counts the partials written from it
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        xcc &= 7u;
+        const uint64_t inc = 1ull << (8 * xcc);
+        const uint64_t now = __hip_atomic_fetch_add(p.split_ctr + bhc, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+        unsigned total = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) total += (unsigned)(now >> (8 * i)) & 255u;
+        // 0: not last; 1: last; 2: last, and every partial came from this XCD (its L2 holds them)
+        *work = total != (unsigned)p.nsplit ? 0u : (((unsigned)(now >> (8 * xcc)) & 255u) == (unsigned)p.nsplit ? 2u : 1u);
+    }
+    __syncthreads();
+    const unsigned role = *work;
+    if (role == 0u) return;
+    if (tid == 0) __hip_atomic_store(p.split_ctr + bhc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid >= nrows * (kD / 4)) return;
+    {
+        const int rr = tid / (kD / 4), c4 = tid % (kD / 4);
+        float M = -INFINITY, L = 0.f;
+        f4 a = {0.f, 0.f, 0.f, 0.f};
+        if (role == 2u) merge_partials<1>(prs, p.nsplit, pstride, rr, c4, M, L, a);    // L2-coherent loads
+        else merge_partials<kSc1>(prs, p.nsplit, pstride, rr, c4, M, L, a);            // device-coherent loads
+        const int r = row0 + rr;
+        const int h = kvh * p.g + r / p.M, m = r % p.M;
+        const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
+        const h4 ov = {(_Float16)(a[0] / L), (_Float16)(a[1] / L), (_Float16)(a[2] / L), (_Float16)(a[3] / L)};
+        *(h4 *)(p.out + row * kD + 4 * c4) = ov;
+        if (c4 == 0 && p.rowstats) {
+            p.rowstats[2 * row] = M;
+            p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
         }
     }
 }
@@ -547,10 +684,13 @@ int64_t decode_fast_slot_bytes(int kb, int vb, int Gv) {
     return (s + 255) / 256 * 256;
 }
 // LDS of one workgroup: W waves x (NS slots + K meta scratch) + the item
-// counter; the end-of-split merge reuses the rings.
+// counter; the end-of-split merge reuses the rings (slots are >= 4 KiB, so the
+// merge never reaches the item counter, which also carries the last-arrival flag).
+static_assert(kWaves * (kNS * 4096 + kKmetaBytes) >= (2 * kWaves * 16 + kWaves * 16 * kAccRow) * 4,
+              "merge area overlaps the item counter");
 int64_t decode_fast_lds_bytes(int64_t slot) {
-    const int64_t ring = kWaves * (kNS * slot + kKmetaBytes) + 16;
-    const int64_t merge = (int64_t)(2 * kWaves * 16 + kWaves * 16 * kD) * 4;
+    const int64_t ring = kWaves * (kNS * slot + kKmetaBytes) + 16 + kQldsBytes;
+    const int64_t merge = (int64_t)(2 * kWaves * 16 + kWaves * 16 * kAccRow) * 4;
     return ring > merge ? ring : merge;
 }
 int decode_fast_waves() { return kWaves; }
@@ -562,7 +702,7 @@ bool decode_fast_eligible(const DecodeParams &p, int wk) {
 
 template <int BK, int BV, int NG, int NS>
 static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
-    dim3 grid(p.nsplit, p.Hkv, p.B * p.nchunk);
+    const dim3 grid((unsigned)(p.nsplit * p.Hkv * p.B * p.nchunk));  // decoded in the kernel
     const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes);
     static bool attr_set = false;  // raise the dynamic LDS cap above 64 KiB once
     if (!attr_set) {

@@ -105,7 +105,9 @@ typedef struct akv_decode_args {
     int64_t n_scores;
     float decay;
     int32_t num_splits;    /* 0 = choose */
-    void *workspace;       /* device scratch, akv_decode_workspace_bytes() bytes */
+    void *workspace;       /* device scratch, akv_decode_workspace_bytes() bytes, zero-filled before its
+                              first use; every call leaves it reusable (its split arrival counters return
+                              to zero), so one workspace serves any number of calls, not concurrent ones */
     int64_t workspace_bytes;
 } akv_decode_args;
 
