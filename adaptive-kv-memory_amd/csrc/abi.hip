@@ -57,8 +57,13 @@ constexpr int kFusedMaxSplits = 32;
 
 bool fast_path(const akv_decode_args *a) {
     const akv_warm_desc &w = a->warm;
-    return w.kind == AKV_WARM_AFFINE && a->D == 128 && w.block_t % 32 == 0 && w.n_out == 0 &&
-           (w.group_v == 32 || w.group_v == 64 || w.group_v == 128);
+    if (!(w.kind == AKV_WARM_AFFINE && a->D == 128 && w.block_t % 32 == 0 &&
+          (w.group_v == 32 || w.group_v == 64 || w.group_v == 128)))
+        return false;
+    // outlier channels: up to 4 per block with 32-channel V groups, when the slot fits the LDS
+    return w.n_out == 0 ||
+           (w.n_out <= 4 && w.group_v == 32 && w.k_odata && w.v_odata && w.k_oidx && w.v_oidx &&
+            akv::decode_fast_lds_bytes(akv::decode_fast_slot_bytes(w.bits_k, w.bits_v, w.group_v, w.n_out), w.n_out) <= 160 * 1024);
 }
 
 void make_plan(const akv_decode_args *a, Plan *pl) {
@@ -84,7 +89,7 @@ void make_plan(const akv_decode_args *a, Plan *pl) {
         // its waves share the range's hot tiles and warm units dynamically.
         const int64_t units = (nw + 31) / 32, tiles = (nh + 15) / 16;
         int64_t cp = a->num_splits > 0 ? a->num_splits : kCUs / pairs;
-        const int64_t by_items = (units + tiles) / (2 * akv::decode_fast_waves());
+        const int64_t by_items = (units + tiles) / (2 * akv::decode_fast_waves(w.n_out));
         if (a->num_splits <= 0 && cp > by_items) cp = by_items;
         if (cp < 1) cp = 1;
         pl->wsplit_len = (units + cp - 1) / cp * 32;
@@ -349,7 +354,7 @@ int akv_decode_attn(const akv_decode_args *a, void *stream) {
     p.scores = a->scores;
     p.n_scores = a->scores ? a->n_scores : 0;
     p.decay = a->decay;
-    if (w.kind == AKV_WARM_AFFINE) p.slot_bytes = (int)akv::decode_fast_slot_bytes(kb, vb, w.group_v);
+    if (w.kind == AKV_WARM_AFFINE) p.slot_bytes = (int)akv::decode_fast_slot_bytes(kb, vb, w.group_v, w.n_out);
     hipError_t e = akv::decode_launch(p, kb, vb, wk, sym_ptr, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     return ok();

@@ -63,9 +63,9 @@ hipError_t decode_reduce_launch(const DecodeParams &p, hipStream_t s);
 
 // LDS-streamed split kernel for the block-affine tier (decode_fast.hip).
 bool decode_fast_eligible(const DecodeParams &p, int wk);
-int64_t decode_fast_slot_bytes(int kb, int vb, int Gv);
-int64_t decode_fast_lds_bytes(int64_t slot_bytes);
-int decode_fast_waves();
+int64_t decode_fast_slot_bytes(int kb, int vb, int Gv, int n_out);
+int64_t decode_fast_lds_bytes(int64_t slot_bytes, int n_out);
+int decode_fast_waves(int n_out);
 hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, hipStream_t s);
 
 }  // namespace akv

@@ -60,30 +60,47 @@ constexpr int kD = 128;
 constexpr int kWaves = AKV_FAST_WAVES;  // waves per workgroup (one workgroup per CU, 3 per SIMD)
 constexpr int kUnit = 32;               // warm tokens per ring slot
 constexpr int kNS = AKV_FAST_NS;        // ring slots per wave (deeper rings only lengthen the tail)
+// With outlier channels the kernel holds more state per lane: 8 waves (2 per
+// SIMD, twice the registers each) with 3 ring slots each.
+#ifndef AKV_FAST_WAVES_OUT
+#define AKV_FAST_WAVES_OUT 8
+#endif
+#ifndef AKV_FAST_NS_OUT
+#define AKV_FAST_NS_OUT 3
+#endif
+constexpr int kWavesOut = AKV_FAST_WAVES_OUT, kNSOut = AKV_FAST_NS_OUT;
+template <bool OUT> struct FastCfg {
+    static constexpr int NW = OUT ? kWavesOut : kWaves, NS = OUT ? kNSOut : kNS;
+};
 constexpr int kLdsCap = 160 * 1024;  // LDS of one CU
 constexpr int kKmetaBytes = 3 * 4 * 16 * 4;  // [s | n | z][group][pair] u32
 constexpr int kHotLoads = 4;         // 16 tokens x 256 B = 4 KiB = 4 wave loads
 constexpr int kQldsBytes = 4 * 64 * 16;  // Q operand of the workgroup
 constexpr int kAccRow = kD + 4;      // fp32 row of the end-of-split merge in LDS (the pad spreads a
                                      // wave's 64 row/chunk writes over the banks)
-template <int BK, int BV, int NG>
+constexpr int kMaxOut = 4;            // outlier channels per block the fast kernel takes
+constexpr int kOutBytes = 2 * (kUnit * kMaxOut * 2) + 2 * 32;  // K/V outlier values + K/V indices
+template <int BK, int BV, int NG, bool OUT>
 struct WarmLayout {
     static constexpr int KR = 16 * BK, VR = 16 * BV;  // packed row bytes (D = 128)
     static constexpr int KCB = kUnit * KR, VCB = kUnit * VR;
     static constexpr int VMB = 64 * NG;               // V scale (or zero) bytes of 32 tokens
     static constexpr int NKC = (KCB + 1023) / 1024, NVC = (VCB + 1023) / 1024;
-    static constexpr int NLOAD = NKC + NVC + 4;
+    static constexpr int NLOAD = NKC + NVC + 4 + (OUT ? 4 : 0);
     static constexpr int KC = 0, VC = KCB, KS = KCB + VCB, KZ = KS + 256, VS = KZ + 256, VZ = VS + VMB;
-    static constexpr int BYTES = VZ + VMB;
+    // outlier channels: fp16 values [token][n_out] of K and V, int64 channel indices of the block
+    static constexpr int KO = VZ + VMB, VO = KO + kUnit * kMaxOut * 2, KI = VO + kUnit * kMaxOut * 2, VI = KI + 32;
+    static constexpr int BYTES = OUT ? VI + 32 : VZ + VMB;
 };
 
 struct WarmRes {
     u4 kc, vc, ks, kz, vs, vz;
+    u4 ko, vo, ki, vi;  // outlier values and indices
 };
 
-template <int BK, int BV, int NG>
-__device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T) {
-    using L = WarmLayout<BK, BV, NG>;
+template <int BK, int BV, int NG, bool OUT>
+__device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T, int n_out) {
+    using L = WarmLayout<BK, BV, NG, OUT>;
     const uint32_t v16 = (uint32_t)lane * 16u;
     const uint32_t base = lds_addr(slot);
 #pragma unroll
@@ -92,11 +109,20 @@ __device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot
 #pragma unroll
     for (int i = 0; i < L::NVC; ++i)
         dma16(R.vc, base + L::VC + 1024 * i, v16, (uint32_t)u * L::VCB + 1024u * i, lane_mask(L::VCB - 1024 * i));
-    const uint32_t kmrow = (uint32_t)((u * kUnit) / T) * 256u;
+    const uint32_t blk = (uint32_t)((u * kUnit) / T);
+    const uint32_t kmrow = blk * 256u;
     dma16(R.ks, base + L::KS, v16, kmrow, 0xFFFFull);
     dma16(R.kz, base + L::KZ, v16, kmrow, 0xFFFFull);
     dma16(R.vs, base + L::VS, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
     dma16(R.vz, base + L::VZ, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+    if (OUT) {
+        const uint32_t ob = (uint32_t)(kUnit * n_out * 2);  // 64 n_out bytes of values per unit
+        const uint64_t im = lane_mask((n_out * 8 + 15) & ~15);
+        dma16(R.ko, base + L::KO, v16, (uint32_t)u * ob, lane_mask((int)ob));
+        dma16(R.vo, base + L::VO, v16, (uint32_t)u * ob, lane_mask((int)ob));
+        dma16(R.ki, base + L::KI, v16, blk * (uint32_t)(n_out * 8), im);
+        dma16(R.vi, base + L::VI, v16, blk * (uint32_t)(n_out * 8), im);
+    }
 }
 
 __device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, int tile) {
@@ -155,9 +181,6 @@ __device__ __forceinline__ void merge_partials(__amdgpu_buffer_rsrc_t prs, int n
 // Work item kinds of a ring slot.
 constexpr int kNone = 0, kWarm = 1, kHotK = 2, kHotV = 3;
 
-#ifndef AKV_FAST_WAVES_PER_EU
-#define AKV_FAST_WAVES_PER_EU (AKV_FAST_WAVES / 4)
-#endif
 // Loads still in flight behind the oldest ring slot, given how many of the
 // younger slots hold a warm unit (nw) or a hot half (nh); nw + nh <= MAXY.
 template <int NLW, int NLH, int MAXY, int W = 0, int H = 0>
@@ -173,11 +196,13 @@ __device__ __forceinline__ void wait_younger(int nw, int nh) {
     else wait_vm<0>();
 }
 
-template <int BK, int BV, int NG, int NS>
-__global__ __launch_bounds__(64 * kWaves) __attribute__((amdgpu_waves_per_eu(AKV_FAST_WAVES_PER_EU, AKV_FAST_WAVES_PER_EU)))
+template <int BK, int BV, int NG, int NS, bool OUT>
+__global__ __launch_bounds__(64 * FastCfg<OUT>::NW)
+__attribute__((amdgpu_waves_per_eu(FastCfg<OUT>::NW / 4, FastCfg<OUT>::NW / 4)))
 void decode_fast_kernel(const DecodeParams p) {
+    constexpr int NW = FastCfg<OUT>::NW;  // waves of the workgroup
     static_assert(NS >= 2 && NS <= 4, "ring depth");
-    using L = WarmLayout<BK, BV, NG>;
+    using L = WarmLayout<BK, BV, NG, OUT>;
     constexpr int KSTEPS = kD / 32;
     constexpr int NLW = L::NLOAD;     // loads of a warm unit
     constexpr int NLH = kHotLoads;    // loads of a hot half
@@ -204,9 +229,11 @@ void decode_fast_kernel(const DecodeParams p) {
     const int slot_bytes = p.slot_bytes;
     unsigned char *ring = smem + wave * (NS * slot_bytes + kKmetaBytes);
     unsigned char *kmeta = ring + NS * slot_bytes;
-    unsigned *work = (unsigned *)(smem + kWaves * (NS * slot_bytes + kKmetaBytes));  // item counter
+    unsigned *work = (unsigned *)(smem + NW * (NS * slot_bytes + kKmetaBytes));  // item counter
     // Q operand of the QK MFMAs, [step][lane] x 16 B, shared by the waves
-    u4 *qlds = (u4 *)(smem + kWaves * (NS * slot_bytes + kKmetaBytes) + 16);
+    u4 *qlds = (u4 *)(smem + NW * (NS * slot_bytes + kKmetaBytes) + 16);
+    // the 16 query rows in natural channel order (fp16): outlier-channel corrections
+    const _Float16 *qn_lds = (const _Float16 *)((unsigned char *)qlds + kQldsBytes);
 
     const int r = row0 + col;
     const int row_valid = col < nrows;
@@ -226,8 +253,8 @@ void decode_fast_kernel(const DecodeParams p) {
     const int u_first = w_begin / kUnit, n_wu = w_end > w_begin ? (w_end + kUnit - 1) / kUnit - u_first : 0;
     const int t_first = h_begin / 16, n_ht = h_end > h_begin ? (h_end + 15) / 16 - t_first : 0;
     const int n_items = n_wu + n_ht;
-    // items 0 .. kWaves-1 go to waves 0 .. kWaves-1; the counter hands out the rest
-    if (threadIdx.x == 0) *work = (unsigned)kWaves;
+    // items 0 .. NW-1 go to waves 0 .. NW-1; the counter hands out the rest
+    if (threadIdx.x == 0) *work = (unsigned)NW;
 
     WarmRes R;
     {
@@ -238,6 +265,13 @@ void decode_fast_kernel(const DecodeParams p) {
         R.kz = rsrc4((const _Float16 *)p.kz + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
         R.vs = rsrc4((const _Float16 *)p.vs + bh * p.n_warm * NG, nwu * NG * 2);
         R.vz = rsrc4((const _Float16 *)p.vz + bh * p.n_warm * NG, nwu * NG * 2);
+        if (OUT) {
+            const int no = p.n_out;
+            R.ko = rsrc4(p.k_odata + bh * p.n_warm * no, nwu * (uint32_t)no * 2);
+            R.vo = rsrc4(p.v_odata + bh * p.n_warm * no, nwu * (uint32_t)no * 2);
+            R.ki = rsrc4(p.k_oidx + (int64_t)b * p.nblk * no, (uint32_t)(p.nblk * no * 8));
+            R.vi = rsrc4(p.v_oidx + (int64_t)b * p.nblk * no, (uint32_t)(p.nblk * no * 8));
+        }
     }
     const u4 rkh = rsrc4(p.khot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
     const u4 rvh = rsrc4(p.vhot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
@@ -272,7 +306,7 @@ void decode_fast_kernel(const DecodeParams p) {
         }
     };
     auto issue = [&](int k, int id, unsigned char *slot) {
-        if (k == kWarm) issue_warm<BK, BV, NG>(R, slot, lane, id, p.T);
+        if (k == kWarm) issue_warm<BK, BV, NG, OUT>(R, slot, lane, id, p.T, p.n_out);
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
@@ -295,6 +329,11 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
         for (int st = 0; st < KSTEPS; ++st)
             qlds[st * 64 + lane] = (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]};
+        if (OUT) {
+            u4 *qn = (u4 *)qn_lds + col * 16 + grp * 4;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) qn[q4] = (u4){nat[4 * q4], nat[4 * q4 + 1], nat[4 * q4 + 2], nat[4 * q4 + 3]};
+        }
     }
     // Only the first slot is filled up front: every wave's first unit is in
     // the memory queue before any wave's second, so compute starts as soon as
@@ -437,6 +476,48 @@ void decode_fast_kernel(const DecodeParams p) {
                 }
             }
 
+            // ---- outlier channels of K: the stored fp16 value replaces the dequantized one,
+            //      so q[c] * (value - dequant) joins the dot product.  A channel the
+            //      quantizer zeroed has scale = zero = 0 and dequantizes to 0, which skips
+            //      the code lookup (taken only when some outlier channel has other meta).
+            if constexpr (OUT) {
+                const int no = p.n_out;
+                const int *ki = (const int *)(slot + L::KI);  // low words of the int64 indices
+                bool lookup = false;
+                for (int o = 0; o < no; ++o) {
+                    const int c = min(max(ki[2 * o], 0), kD - 1);
+                    lookup |= *(const _Float16 *)(slot + L::KS + 2 * c) != (_Float16)0 ||
+                              *(const _Float16 *)(slot + L::KZ + 2 * c) != (_Float16)0;
+                }
+                if (!__builtin_amdgcn_ballot_w64(lookup) && no == 1) {
+                    const int c = min(max(ki[0], 0), kD - 1);
+                    const float qd = (float)qn_lds[col * kD + c];
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const h4 od = *(const h4 *)(slot + L::KO + 2 * (16 * h + 4 * grp));  // tokens 4 grp .. +3
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) sc[h][i] += qd * (float)od[i];
+                    }
+                } else {
+                    for (int o = 0; o < no; ++o) {
+                        const int c = min(max(ki[2 * o], 0), kD - 1);
+                        const _Float16 s_c = *(const _Float16 *)(slot + L::KS + 2 * c);
+                        const _Float16 z_c = *(const _Float16 *)(slot + L::KZ + 2 * c);
+                        const float qd = (float)qn_lds[col * kD + c];
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int t = 16 * h + 4 * grp + i;
+                                const float od = (float)*(const _Float16 *)(slot + L::KO + 2 * (t * no + o));
+                                const uint32_t code = extract_code(slot + L::KC + t * L::KR, c, BK);
+                                const float kd = (float)(_Float16)((_Float16)((_Float16)(float)code * s_c) + z_c);
+                                sc[h][i] += qd * (od - kd);
+                            }
+                    }
+                }
+            }
+
             // ---- softmax over the 32 tokens (ragged tail masked; logits stashed)
             if (tok0 + kUnit > nw) {
 #pragma unroll
@@ -521,6 +602,61 @@ void decode_fast_kernel(const DecodeParams p) {
             }
             stt.accz = mfma_k32(__builtin_bit_cast(h8, (u4){as_u32(vz[0][0]), as_u32(vz[0][1]), as_u32(vz[1][0]), as_u32(vz[1][1])}),
                                 pop, stt.accz);
+            // ---- outlier channels of V: channel c of chunk c/8 took round16(code s) + z
+            //      (z through accz); three exact MFMAs add sum_t P (value - round16(code s) - z)
+            //      to its accumulator, in the lanes of that chunk only
+            if constexpr (OUT) {
+                const int no = p.n_out;
+                const int *vi = (const int *)(slot + L::VI);
+                for (int o = 0; o < no; ++o) {
+                    const int c = min(max(vi[2 * o], 0), kD - 1);
+                    const bool gsel = col == (c >> 3);
+                    uint32_t av[4], az[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int h = q >> 1, pp = q & 1, t = 16 * h + 4 * grp + 2 * pp;
+                        const uint32_t ov = no == 1 ? *(const uint32_t *)(slot + L::VO + 2 * t)
+                                                    : as_u32(lds_h2(slot + L::VO + 2 * (t * no + o),
+                                                                    slot + L::VO + 2 * ((t + 1) * no + o)));
+                        av[q] = gsel ? ov : 0u;
+                        az[q] = gsel ? (as_u32(vz[h][pp]) ^ 0x80008000u) : 0u;
+                    }
+                    // the code of channel c for the lane's token pairs, selected at run time
+                    // (offset and window are uniform), then round16(code s) exactly
+                    const int kk = c & 7, off = voff<BV>(kk), wsel = vwin<BV>(kk);
+                    const uint32_t msk = (((1u << BV) - 1u) << off) * 0x00010001u;
+                    const _Float16 mv = (_Float16)magic_val(off);
+                    uint32_t ad[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int h = q >> 1, pp = q & 1;
+                        uint32_t wv = win[h][pp][0];
+#pragma unroll
+                        for (int wi = 1; wi < VSlot<BV>::NW; ++wi) wv = wsel == wi ? win[h][pp][wi] : wv;
+                        const uint32_t uu = (wv & msk) | magic2(off);
+                        const h2 d = (as_h2(uu) - (h2){mv, mv}) * vs[h][pp];
+                        ad[q] = gsel ? (as_u32(d) ^ 0x80008000u) : 0u;
+                    }
+                    const h8 a1 = __builtin_bit_cast(h8, (u4){av[0], av[1], av[2], av[3]});
+                    const h8 a2 = __builtin_bit_cast(h8, (u4){ad[0], ad[1], ad[2], ad[3]});
+                    const h8 a3 = __builtin_bit_cast(h8, (u4){az[0], az[1], az[2], az[3]});
+                    auto fix = [&](f4 &acc) {
+                        acc = mfma_k32(a1, pop, acc);
+                        acc = mfma_k32(a2, pop, acc);
+                        acc = mfma_k32(a3, pop, acc);
+                    };
+                    switch (kk) {
+                        case 0: fix(stt.acc[0]); break;
+                        case 1: fix(stt.acc[1]); break;
+                        case 2: fix(stt.acc[2]); break;
+                        case 3: fix(stt.acc[3]); break;
+                        case 4: fix(stt.acc[4]); break;
+                        case 5: fix(stt.acc[5]); break;
+                        case 6: fix(stt.acc[6]); break;
+                        default: fix(stt.acc[7]); break;
+                    }
+                }
+            }
         } else if (k == kHotK) {
             // ---- hot K tile: 16 tokens x 256 B; lane = (token col, 32 channels of group grp)
             uint32_t nat[16], pairs[16];
@@ -581,14 +717,14 @@ void decode_fast_kernel(const DecodeParams p) {
     stt.l = wsum16(stt.l);
     __syncthreads();
     float *mlds = (float *)smem;                   // [W][16] running maxima
-    float *llds = mlds + kWaves * 16;              // [W][16] rescaled sums
-    float *alds = llds + kWaves * 16;              // [W][16][kAccRow] rescaled accumulators
+    float *llds = mlds + NW * 16;              // [W][16] rescaled sums
+    float *alds = llds + NW * 16;              // [W][16][kAccRow] rescaled accumulators
     if (grp == 0) mlds[wave * 16 + col] = stt.m2;
     __syncthreads();
     {
         float mx = -INFINITY;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, mlds[w * 16 + col]);
+        for (int w = 0; w < NW; ++w) mx = fmaxf(mx, mlds[w * 16 + col]);
         const float fw = (stt.m2 == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(stt.m2 - mx);
         if (grp == 0) llds[wave * 16 + col] = stt.l * fw;
 #pragma unroll
@@ -608,18 +744,18 @@ void decode_fast_kernel(const DecodeParams p) {
     const __amdgpu_buffer_rsrc_t prs = make_rsrc(p.part + bhc * p.nsplit * pstride, (uint32_t)(p.nsplit * pstride * 4));
     constexpr int kSc1 = 16;  // cache-policy bit sc1: coherent at device scope
     const int tid = threadIdx.x;
-    if (tid < nrows * (kD / 4)) {  // thread = (row, channel quad); 512 <= 64 * kWaves
+    if (tid < nrows * (kD / 4)) {  // thread = (row, channel quad); 512 <= 64 * NW
         const int rr = tid / (kD / 4), c4 = tid % (kD / 4);
         f4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) a += *(const f4 *)(alds + (w * 16 + rr) * kAccRow + 4 * c4);
+        for (int w = 0; w < NW; ++w) a += *(const f4 *)(alds + (w * 16 + rr) * kAccRow + 4 * c4);
         const int off = (int)((split * pstride + rr * PS) * 4);
         if (fused) __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, a), prs, off + 16 + 16 * c4, 0, kSc1);
         else *(f4 *)(part + rr * PS + 4 + 4 * c4) = a;
         if (c4 == 0) {
             float mx = -INFINITY, l = 0.f;
 #pragma unroll
-            for (int w = 0; w < kWaves; ++w) {
+            for (int w = 0; w < NW; ++w) {
                 mx = fmaxf(mx, mlds[w * 16 + rr]);
                 l += llds[w * 16 + rr];
             }
@@ -677,9 +813,9 @@ void decode_fast_kernel(const DecodeParams p) {
 }
 
 // LDS slot of the fast kernel: one warm unit, or one 16-token hot K or V half.
-int64_t decode_fast_slot_bytes(int kb, int vb, int Gv) {
+int64_t decode_fast_slot_bytes(int kb, int vb, int Gv, int n_out) {
     const int NG = kD / Gv;
-    int64_t warm = (int64_t)kUnit * 16 * (kb + vb) + 512 + 128 * NG;
+    int64_t warm = (int64_t)kUnit * 16 * (kb + vb) + 512 + 128 * NG + (n_out > 0 ? kOutBytes : 0);
     int64_t s = warm > 4096 ? warm : 4096;
     return (s + 255) / 256 * 256;
 }
@@ -688,40 +824,47 @@ int64_t decode_fast_slot_bytes(int kb, int vb, int Gv) {
 // merge never reaches the item counter, which also carries the last-arrival flag).
 static_assert(kWaves * (kNS * 4096 + kKmetaBytes) >= (2 * kWaves * 16 + kWaves * 16 * kAccRow) * 4,
               "merge area overlaps the item counter");
-int64_t decode_fast_lds_bytes(int64_t slot) {
-    const int64_t ring = kWaves * (kNS * slot + kKmetaBytes) + 16 + kQldsBytes;
-    const int64_t merge = (int64_t)(2 * kWaves * 16 + kWaves * 16 * kAccRow) * 4;
+static_assert(kWavesOut * (kNSOut * 4096 + kKmetaBytes) >= (2 * kWavesOut * 16 + kWavesOut * 16 * kAccRow) * 4,
+              "merge area overlaps the item counter");
+int64_t decode_fast_lds_bytes(int64_t slot, int n_out) {
+    const int nw = n_out > 0 ? kWavesOut : kWaves, ns = n_out > 0 ? kNSOut : kNS;
+    const int64_t ring = nw * (ns * slot + kKmetaBytes) + 16 + 2 * kQldsBytes;
+    const int64_t merge = (int64_t)(2 * nw * 16 + nw * 16 * kAccRow) * 4;
     return ring > merge ? ring : merge;
 }
-int decode_fast_waves() { return kWaves; }
+int decode_fast_waves(int n_out) { return n_out > 0 ? kWavesOut : kWaves; }
 
 bool decode_fast_eligible(const DecodeParams &p, int wk) {
-    return wk == AKV_WARM_AFFINE && p.D == kD && p.T % kUnit == 0 && p.n_out == 0 &&
-           (p.Gv == 32 || p.Gv == 64 || p.Gv == 128);
+    if (!(wk == AKV_WARM_AFFINE && p.D == kD && p.T % kUnit == 0 && (p.Gv == 32 || p.Gv == 64 || p.Gv == 128)))
+        return false;
+    // outlier channels: up to kMaxOut per block, V groups of 32 channels
+    return p.n_out == 0 || (p.n_out <= kMaxOut && p.Gv == 32 && p.k_odata && p.v_odata && p.k_oidx && p.v_oidx &&
+                            decode_fast_lds_bytes(p.slot_bytes, p.n_out) <= kLdsCap);
 }
 
-template <int BK, int BV, int NG, int NS>
+template <int BK, int BV, int NG, int NS, bool OUT>
 static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
     const dim3 grid((unsigned)(p.nsplit * p.Hkv * p.B * p.nchunk));  // decoded in the kernel
-    const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes);
+    const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes, OUT ? p.n_out : 0);
     static bool attr_set = false;  // raise the dynamic LDS cap above 64 KiB once
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS>,
+        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS, OUT>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCap);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG, NS>), grid, dim3(64 * kWaves), lds, s, p);
+    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG, NS, OUT>), grid, dim3(64 * FastCfg<OUT>::NW), lds, s, p);
     return hipGetLastError();
 }
 
 template <int BK, int BV, int NG>
 static hipError_t launch_fast(const DecodeParams &p, hipStream_t s) {
-    return launch_fast_ns<BK, BV, NG, kNS>(p, s);
+    return launch_fast_ns<BK, BV, NG, kNS, false>(p, s);
 }
 
 template <int BK, int BV>
 static hipError_t launch_fast_ng(const DecodeParams &p, hipStream_t s) {
+    if (p.n_out > 0) return p.Gv == 32 ? launch_fast_ns<BK, BV, 4, kNSOut, true>(p, s) : hipErrorInvalidValue;
     if (p.Gv == 32) return launch_fast<BK, BV, 4>(p, s);
     if (p.Gv == 64) return launch_fast<BK, BV, 2>(p, s);
     if (p.Gv == 128) return launch_fast<BK, BV, 1>(p, s);

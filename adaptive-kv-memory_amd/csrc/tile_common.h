@@ -31,6 +31,7 @@ __device__ __forceinline__ u4 rsrc4(const void *base, uint32_t bytes) {
 // resource range arrive as zeros.  Written as one asm block so the compiler
 // can neither merge two of them under divergent control flow nor change how
 // many are issued (the vmcnt waits count them); M0 is restored afterwards.
+// M0 is written several instructions before the load that reads it.
 __device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff, uint64_t mask) {
     uint64_t saved;
     uint32_t saved_m0;
@@ -173,13 +174,16 @@ __host__ __device__ constexpr int v_ostep() { return BV == 3 ? 3 : (BV == 4 ? 4 
 template <int BV>
 __host__ __device__ constexpr int v_noffs() { return BV == 3 ? 3 : (BV == 4 ? 2 : 4); }
 
-// Masks of a code at bit offset o (both halves), one VGPR per offset 0..7.
+// Masks of a code at bit offset o (both halves), one VGPR per offset the bit
+// width uses (3 bits: any of 0..7; 4 bits: 0, 4; 2 bits: 0, 2, 4, 6).
 template <int B>
 struct Masks {
     uint32_t m[8];
     __device__ __forceinline__ void init() {
 #pragma unroll
-        for (int o = 0; o < 8; ++o) m[o] = in_vgpr((((1u << B) - 1u) << o) * 0x00010001u);
+        for (int o = 0; o < 8; ++o)
+            if (B == 3 || (B == 4 && o % 4 == 0) || (B == 2 && o % 2 == 0))
+                m[o] = in_vgpr((((1u << B) - 1u) << o) * 0x00010001u);
     }
 };
 

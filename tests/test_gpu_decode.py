@@ -88,6 +88,40 @@ def test_outlier_channels_heavy_tails():
     assert_close_attn(out, ref)
 
 
+@pytest.mark.parametrize("bk,bv,of", [(4, 2, 0.01), (3, 3, 0.02), (2, 4, 0.03), (4, 4, 0.01)])
+def test_fast_outlier_channels(bk, bv, of):
+    """Outlier channels on the LDS-streamed kernel (D=128, T=32, G=32): up to
+    four fp16 channels per block replace the dequantized K and V values."""
+    announce(f"decode fast path outliers bits={bk}/{bv} fraction={of}")
+    q, kh, vh, w, kd, vd = _case(2, 8, 4, 128, 80, 700, bk, bv, of=of, outl=0, heavy=4, seed=7)
+    assert w["n_out"] == max(1, int(128 * of))
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
+
+
+def test_fast_outliers_nonzero_meta():
+    """The stored values replace whatever the codes at an outlier channel
+    dequantize to: with the channel's K scale / zero made non-zero and random
+    codes there, the output must not change (the kernel looks the codes up)."""
+    announce("decode fast path outliers with non-zero meta at the outlier channels")
+    q, kh, vh, w, kd, vd = _case(1, 4, 2, 128, 48, 320, 4, 2, of=0.02, outl=0, heavy=2, seed=8)
+    rng = np.random.default_rng(1)
+    w = dict(w)
+    ks, kz = w["k_scale"].copy(), w["k_zero"].copy()
+    for b in range(ks.shape[0]):
+        for blk in range(ks.shape[2]):
+            for c in w["k_oidx"][b, blk]:
+                ks[b, :, blk, c] = rng.uniform(0.05, 0.5, ks.shape[1]).astype(np.float16)
+                kz[b, :, blk, c] = rng.uniform(-1.0, 1.0, ks.shape[1]).astype(np.float16)
+    w["k_scale"], w["k_zero"] = ks, kz
+    w["k_codes"] = rng.integers(0, 256, w["k_codes"].shape, dtype=np.uint8)
+    kd2, vd2 = oaff.dequant_kv_blocked(w)
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd2, vd2, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
+
+
 @pytest.mark.parametrize("D", [64])
 def test_head_dim_64(D):
     announce("decode D=64")
