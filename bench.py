@@ -15,10 +15,10 @@ plus us_per_layer, the roofline of the dequant-attention op and the CPU
 baseline (the oracle's restatement of the reference CPU path on a bounded
 sample).
 
-The roofline is taken on the attention-only replay (per layer: the split
-kernel decode_fast_kernel, which carries ~85% of the time, and the split
-merge): achieved = the op's algorithmic bytes / its per-layer time, from HIP
-events on the stream the kernels run on.  `traffic` (HBM bytes per layer of
+The roofline is taken on the attention-only replay (per layer: one launch of
+decode_fast_kernel, which also merges its splits): achieved = the op's
+algorithmic bytes / its per-layer time, from HIP events on the stream the
+kernel runs on.  `traffic` (HBM bytes per layer of
 that op) comes from the FETCH_SIZE / WRITE_SIZE counter runs recorded in
 profiles/decode_qwen_decode_32k_traffic.json, scaled by the same counters on
 a copy of known size (--calib-copy adds that copy to the run).
@@ -202,7 +202,7 @@ def main():
         "hbm_frac_effective_kv": round(kv_gbps / HBM_PEAK_GBPS, 4),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": "akv_decode_attn attention per layer (decode_fast_kernel + decode_reduce_kernel)",
+                     "kernel": "akv_decode_attn attention per layer (decode_fast_kernel, splits merged in the kernel)",
                      "algorithmic_bytes_per_launch": alg,
                      "us_per_launch": round(us_layer_attn, 3)},
     }
@@ -281,7 +281,7 @@ def bench_decode_mha(args):
            "us_per_layer": round(us_layer, 3),
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                        "kernel": "akv_decode_attn per layer (decode_split_kernel + decode_reduce_kernel)",
+                        "kernel": "akv_decode_attn per layer (decode_fast_kernel with outlier channels)",
                         "algorithmic_bytes_per_launch": alg, "us_per_launch": round(us_layer, 3)}}
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(layers[0], s, budget_s=15.0)
