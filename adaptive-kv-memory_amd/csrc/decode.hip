@@ -838,6 +838,83 @@ __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodePar
     }
 }
 
+// Attention weights and importance EMA from the logit stash and the row
+// statistics written by the fast kernel's in-kernel split merge.  Workgroup =
+// 64 tokens; thread (token quad q, row lane rl) reads 4 consecutive tokens of
+// rows rl, rl + 16, ... (16-byte loads when the rows are 16-byte aligned); the
+// row statistics come with the same batch of loads.  Same arithmetic and
+// summation order as finish_kernel.
+template <bool VEC>
+__global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p) {
+    __shared__ float red[16][65];
+    const int tid = threadIdx.x, q = tid & 15, rl = tid >> 4;
+    const int64_t rows = (int64_t)p.B * p.Hq * p.M, N = p.N;
+    const int64_t n0 = (int64_t)blockIdx.x * 64 + 4 * q;
+    float imp[4] = {0.f, 0.f, 0.f, 0.f};
+    constexpr int RB = 8;  // rows per batch of loads
+    for (int64_t r0 = rl; r0 < rows; r0 += 16 * RB) {
+        f4 x[RB];
+        float M[RB], W[RB];
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int64_t r = r0 + 16 * j;
+            M[j] = -INFINITY;
+            W[j] = 0.f;
+            x[j] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+            if (r < rows) {
+                M[j] = p.rowstats[2 * r];
+                W[j] = 1.0f / p.rowstats[2 * r + 1];
+                const float *src = p.stash + r * N + n0;
+                if (VEC && n0 + 3 < N) {
+                    x[j] = *(const f4 *)src;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (n0 + i < N) x[j][i] = src[i];
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const int64_t r = r0 + 16 * j;
+            if (r >= rows) break;
+            f4 w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float e = (M[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[j][i] - M[j]);
+                w[i] = e * W[j];
+                if (n0 + i < N) imp[i] += w[i];
+            }
+            if (p.attn_out) {
+                float *dst = p.stash + r * N + n0;
+                if (VEC && n0 + 3 < N) {
+                    *(f4 *)dst = w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (n0 + i < N) dst[i] = w[i];
+                }
+            }
+        }
+    }
+    if (!p.scores) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) red[rl][4 * q + i] = imp[i];
+    __syncthreads();
+    if (tid < 64) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) sacc += red[k][tid];
+        const int64_t n = (int64_t)blockIdx.x * 64 + tid;
+        if (n < p.n_scores) {
+            // mean over (batch, head), summed over query positions
+            float sc = p.scores[n] * p.decay;
+            sc = sc + sacc / (float)(p.B * p.Hq);
+            p.scores[n] = sc;
+        }
+    }
+}
+
 // Split merge + attention weights / importance EMA in one launch (the stash
 // path).  Every workgroup first rebuilds the statistics of every query row
 // from the split partials -- M = max_s m_s, L = sum_s 2^(m_s - M) l_s (x 2^7)
@@ -1025,6 +1102,14 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
     else e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M;
+    if (p.stash && p.split_ctr) {
+        // the split kernel merged its splits and wrote the row statistics
+        const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
+        const dim3 g((unsigned)((nmax + 63) / 64));
+        if (p.N % 4 == 0) hipLaunchKernelGGL(weights_stats_kernel<true>, g, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(weights_stats_kernel<false>, g, dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
     if (p.stash && rows <= kFinishRows) {
         // one launch: output merge (unless the split kernel did it) + weights / importance
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;

@@ -132,10 +132,16 @@ __device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, i
         dma16(r, base + 1024 * i, (uint32_t)lane * 16u, (uint32_t)tile * 4096u + 1024u * i, ~0ull);
 }
 
+// Logits of 4 consecutive tokens of one row (log2 domain): one 16-byte store when
+// all 4 are valid and the row offset is 16-byte aligned (vec), else one per token.
 __device__ __forceinline__ void stash4(const DecodeParams &p, int64_t strow, int row_valid, int64_t n0, f4 s,
-                                       float sl2, int nvalid) {
+                                       float sl2, int nvalid, bool vec) {
     if (!p.stash || !row_valid) return;
     float *dst = p.stash + strow + n0;
+    if (vec && nvalid >= 4) {
+        *(f4 *)dst = s * sl2;
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
         if (i < nvalid) dst[i] = s[i] * sl2;
@@ -244,6 +250,8 @@ void decode_fast_kernel(const DecodeParams p) {
     const float sl2 = p.scale_log2;
     const int64_t warm_base = p.hot_first ? p.n_hot : 0;  // logical position of warm token 0
     const int64_t hot_base = p.hot_first ? 0 : p.n_warm;
+    // the stash rows are N floats apart: 16-byte stores need N and the segment base divisible by 4
+    const bool st_vec_w = p.N % 4 == 0 && warm_base % 4 == 0, st_vec_h = p.N % 4 == 0 && hot_base % 4 == 0;
 
     // this workgroup's items: warm 32-token units, then hot 16-token tiles (the
     // cheap hot items come last and even out the waves' finishing times)
@@ -532,7 +540,7 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int t0 = tok0 + 16 * h;
-                    stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], sl2, min(4, nw - (t0 + 4 * grp)));
+                    stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], sl2, min(4, nw - (t0 + 4 * grp)), st_vec_w);
                 }
             }
             const h8 pop = softmax32(stt, sc[0], sc[1], sl2);
@@ -682,7 +690,7 @@ void decode_fast_kernel(const DecodeParams p) {
                 for (int ii = 0; ii < 4; ++ii)
                     if (ii >= nvalid) sh[ii] = -INFINITY;
             }
-            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, sl2, nvalid);
+            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, sl2, nvalid, st_vec_h);
             hot_p = softmax16(stt, sh, sl2);
         } else {
             // ---- hot V tile: lane = (chunk col, tokens 4 grp .. +3)

@@ -59,6 +59,24 @@ def test_weights_and_importance(hot_first):
     np.testing.assert_allclose(sc.cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("Nh,Nw,hot_first", [(37, 700, False), (37, 731, False), (37, 731, True), (3, 61, True)])
+def test_weights_ragged_token_counts(Nh, Nw, hot_first):
+    """Token counts and tier offsets that are not multiples of 4 (scalar stash / weight stores)."""
+    announce(f"decode weights ragged Nh={Nh} Nw={Nw} hot_first={hot_first}")
+    q, kh, vh, w, kd, vd = _case(2, 8, 2, 128, Nh, Nw, 4, 2, seed=11, M=2)
+    N = Nh + Nw
+    scores0 = np.random.default_rng(3).random(N + 5).astype(np.float32)
+    sc = to_dev(scores0)
+    out, attn = _run(q, kh, vh, w, hot_first, scores=sc, decay=0.8, return_weights=True)
+    ref, ref_attn = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=hot_first)
+    assert_close_attn(out, ref)
+    a = attn.cpu().numpy()
+    np.testing.assert_allclose(a, ref_attn, atol=2e-6, rtol=1e-4)
+    np.testing.assert_allclose(a.sum(-1), 1.0, atol=1e-5)
+    ref_sc = oimp.fused_importance_update(ref_attn, scores0, 0.8)
+    np.testing.assert_allclose(sc.cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-6)
+
+
 def test_importance_without_weights_matches():
     announce("decode importance (stash in workspace)")
     q, kh, vh, w, kd, vd = _case(2, 12, 2, 128, 64, 448, 4, 4, seed=2)
