@@ -850,6 +850,9 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
     const int tid = threadIdx.x, q = tid & 15, rl = tid >> 4;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M, N = p.N;
     const int64_t n0 = (int64_t)blockIdx.x * 64 + 4 * q;
+    // the old score is loaded with the first batch of logits, not after the reduction
+    const int64_t ns = (int64_t)blockIdx.x * 64 + tid;
+    const float sc_old = (p.scores && tid < 64 && ns < p.n_scores) ? p.scores[ns] : 0.f;
     float imp[4] = {0.f, 0.f, 0.f, 0.f};
     constexpr int RB = 8;  // rows per batch of loads
     for (int64_t r0 = rl; r0 < rows; r0 += 16 * RB) {
@@ -905,12 +908,11 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
         float sacc = 0.f;
 #pragma unroll
         for (int k = 0; k < 16; ++k) sacc += red[k][tid];
-        const int64_t n = (int64_t)blockIdx.x * 64 + tid;
-        if (n < p.n_scores) {
+        if (ns < p.n_scores) {
             // mean over (batch, head), summed over query positions
-            float sc = p.scores[n] * p.decay;
+            float sc = sc_old * p.decay;
             sc = sc + sacc / (float)(p.B * p.Hq);
-            p.scores[n] = sc;
+            p.scores[ns] = sc;
         }
     }
 }
