@@ -232,10 +232,149 @@ __global__ __launch_bounds__(1024) void select_kernel(const float *scores, int64
     }
 }
 
+// Rows of up to 65536 scores: the same selection with the keys held in
+// registers (element tid + 1024 j in slot j of thread tid), read once.  In the
+// first pass (sign and exponent bits, which cluster) the two most common digits
+// of a wave are added as groups (one LDS atomic each) before the per-lane
+// atomics; the digit searches and the output positions use wave scans (the
+// positions from per-(slot, wave) counts scanned in element order).
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = (uint32_t)__shfl_up((int)x, o);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+constexpr int kSelSlots = 64;
+__global__ __launch_bounds__(1024) void select_reg_kernel(const float *scores, int64_t len, int64_t n, int64_t pf,
+                                                          int64_t pl, int64_t *out) {
+    __shared__ uint32_t hist[16][256];
+    __shared__ uint32_t tot[256];
+    __shared__ uint32_t cnt_lt[1024], cnt_eq[1024];
+    __shared__ uint32_t s_prefix, s_k;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const float *srow = scores + (int64_t)blockIdx.x * len;
+    int64_t *orow = out + (int64_t)blockIdx.x * n;
+    const int64_t rec = len - pl > 0 ? len - pl : 0;
+    uint32_t key[kSelSlots];
+    // buffer loads: the slot offset is a constant, so no per-slot address registers
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(srow, (uint32_t)(len * 4));
+#pragma unroll
+    for (int j = 0; j < kSelSlots; ++j)
+        key[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)tid * 4u, 4096 * j, 0);
+    // 32-bit position arithmetic against per-thread limits (len <= 65536), so that no
+    // per-slot index stays live in a register
+    const int lim = (int)len - tid, lim_pf = (int)pf - tid, lim_rec = (int)rec - tid;
+#pragma unroll
+    for (int j = 0; j < kSelSlots; ++j) {
+        const bool prot = 1024 * j < lim_pf || 1024 * j >= lim_rec;
+        key[j] = 1024 * j < lim ? (prot ? kKeyInf : order_key(__builtin_bit_cast(float, key[j]))) : 0u;
+    }
+    auto valid = [&](int j) { return 1024 * j < lim; };
+    if (tid == 0) {
+        s_prefix = 0u;
+        s_k = (uint32_t)n;
+    }
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        for (int i = tid; i < 16 * 256; i += 1024) (&hist[0][0])[i] = 0u;
+        __syncthreads();
+        const uint32_t prefix = s_prefix;
+        const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
+#pragma unroll
+        for (int j = 0; j < kSelSlots; ++j) {
+            const uint32_t d = (key[j] >> shift) & 255u;
+            bool pend = valid(j) && (key[j] & hmask) == prefix;
+            if (pass == 0) {  // the sign / exponent digit clusters: add the two most common
+                              // digits of the wave as groups, the rest per lane
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const uint64_t act = __builtin_amdgcn_ballot_w64(pend);
+                    if (!act) break;
+                    const int first = (int)__builtin_ctzll(act);
+                    const uint32_t db = (uint32_t)__builtin_amdgcn_readlane((int)d, first);
+                    const uint64_t m = __builtin_amdgcn_ballot_w64(pend && d == db);
+                    if (lane == first) atomicAdd(&hist[wave][db], (uint32_t)__builtin_popcountll(m));
+                    pend = pend && d != db;
+                }
+            }
+            if (pend) atomicAdd(&hist[wave][d], 1u);
+            asm volatile("" ::: "memory");
+        }
+        __syncthreads();
+        // digit of the k-th key: scan of the 256 bin totals (4 waves), then the one
+        // bin with excl < k <= incl (the last bin also when the keys run out)
+        const uint32_t k = s_k;
+        uint32_t t = 0, incl = 0;
+        if (tid < 256) {
+#pragma unroll
+            for (int w = 0; w < 16; ++w) t += hist[w][tid];
+            incl = wave_incl_scan(t, lane);
+            if (lane == 63) tot[wave] = incl;
+        }
+        __syncthreads();
+        if (tid < 256) {
+            for (int w = 0; w < wave; ++w) incl += tot[w];
+            const uint32_t excl = incl - t;
+            if (excl < k && (k <= incl || tid == 255)) {
+                s_k = k - excl;
+                s_prefix = prefix | ((uint32_t)tid << shift);
+            }
+        }
+        __syncthreads();
+    }
+    const uint32_t tau = s_prefix, take_eq = s_k;  // take the first take_eq elements equal to tau
+    // counts of (slot j, wave w) at entry 16 j + w: element order
+#pragma unroll
+    for (int j = 0; j < kSelSlots; ++j) {
+        const uint64_t ml = __builtin_amdgcn_ballot_w64(valid(j) && key[j] < tau);
+        const uint64_t me = __builtin_amdgcn_ballot_w64(valid(j) && key[j] == tau);
+        if (lane == 0) {
+            cnt_lt[16 * j + wave] = (uint32_t)__builtin_popcountll(ml);
+            cnt_eq[16 * j + wave] = (uint32_t)__builtin_popcountll(me);
+        }
+        asm volatile("" ::: "memory");
+    }
+    __syncthreads();
+    {  // exclusive scans of the 1024 counts: in each wave, then across the 16 waves
+        const uint32_t own_lt = cnt_lt[tid], own_eq = cnt_eq[tid];
+        uint32_t il = wave_incl_scan(own_lt, lane), ie = wave_incl_scan(own_eq, lane);
+        if (lane == 63) {
+            hist[0][wave] = il;
+            hist[1][wave] = ie;
+        }
+        __syncthreads();
+        for (int w = 0; w < wave; ++w) {
+            il += hist[0][w];
+            ie += hist[1][w];
+        }
+        cnt_lt[tid] = il - own_lt;
+        cnt_eq[tid] = ie - own_eq;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kSelSlots; ++j) {
+        const bool lt = valid(j) && key[j] < tau, eq = valid(j) && key[j] == tau;
+        const uint64_t ml = __builtin_amdgcn_ballot_w64(lt), me = __builtin_amdgcn_ballot_w64(eq);
+        const uint32_t lt_before = cnt_lt[16 * j + wave] + __builtin_amdgcn_mbcnt_hi((uint32_t)(ml >> 32),
+                                       __builtin_amdgcn_mbcnt_lo((uint32_t)ml, 0u));
+        const uint32_t eq_before = cnt_eq[16 * j + wave] + __builtin_amdgcn_mbcnt_hi((uint32_t)(me >> 32),
+                                       __builtin_amdgcn_mbcnt_lo((uint32_t)me, 0u));
+        const int64_t i = (int64_t)(tid + 1024 * j);
+        if (lt) orow[lt_before + (eq_before < take_eq ? eq_before : take_eq)] = i;
+        else if (eq && eq_before < take_eq) orow[lt_before + eq_before] = i;
+        asm volatile("" ::: "memory");  // one slot at a time (keeps the live ranges short)
+    }
+}
+
 hipError_t select_launch(const float *scores, int64_t rows, int64_t len, int64_t n, int64_t pf, int64_t pl,
                          int64_t *out, hipStream_t s) {
     if (rows <= 0 || n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(1024), 0, s, scores, len, n, pf, pl, out);
+    if (len <= 1024 * kSelSlots)
+        hipLaunchKernelGGL(select_reg_kernel, dim3((unsigned)rows), dim3(1024), 0, s, scores, len, n, pf, pl, out);
+    else
+        hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(1024), 0, s, scores, len, n, pf, pl, out);
     return hipGetLastError();
 }
 
