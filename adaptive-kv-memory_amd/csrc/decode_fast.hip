@@ -2,42 +2,51 @@
 // through LDS: the decode kernel of the 32k-context workload.
 //
 // Scope: head_dim 128, K blocks of T tokens with T a multiple of 32, V groups
-// of G = 32, 64 or 128 channels, no outlier channels, 2/3/4 bits for K and V.
-// Other shapes use decode_split_kernel (decode.hip).
+// of G = 32, 64 or 128 channels, 2/3/4 bits for K and V, and (variant OUT, V
+// groups of 32) up to 4 fp16 outlier channels per block.  Other shapes use
+// decode_split_kernel (decode.hip).
 //
-// Work split: grid (split, kv-head, batch * row-chunk); a workgroup of 4
-// waves owns one (batch, kv-head) and one contiguous token range of either
-// the warm or the hot segment.  Each wave walks its own units (warm: 32-token
-// blocks; hot: the K or the V half of a 16-token tile) round-robin over the
-// range, through a private ring of NS LDS slots filled by buffer loads that
-// write LDS directly (16 B per lane).  A unit's six arrays (K codes, V codes,
-// K scale, K zero, V scale, V zero) are each one contiguous byte range, so a
-// slot fills with 6-8 wave-wide loads whose offsets are scalars; ranges past
-// the end of a (batch, kv-head) read as zero (buffer range check), which
-// keeps ragged tails in bounds.  The loads of units i+1 .. i+NS-1 stay in
-// flight while unit i is computed.
+// Work split: a 1-D grid over (split, kv-head, batch * row-chunk), renumbered
+// so that each XCD gets a contiguous run of items; a workgroup of 12 waves (8
+// for OUT) owns one (batch, kv-head, row chunk of 16 query rows) and one token
+// range: warm 32-token units first, then hot 16-token tiles (each two items:
+// its K and its V half).  A wave takes its first item by its index and the
+// next ones from a workgroup counter in LDS, through a private ring of NS LDS
+// slots filled by buffer loads that write LDS directly (16 B per lane).  A
+// unit's arrays (K codes, V codes, K scale, K zero, V scale, V zero, and the
+// outlier values and indices) are each one contiguous byte range, so a slot
+// fills with a few wave-wide loads whose offsets are scalars; ranges past the
+// end of a (batch, kv-head) read as zero (buffer range check), which keeps
+// ragged tails in bounds.  The loads of the younger slots stay in flight while
+// the oldest is computed.
 //
-// Per 16-token tile a wave does:
-//   QK:  S^T[16 tok x 16 rows] = K . Q^T, 4 x v_mfma_f32_16x16x32_f16.  Lane
-//        (token l%16, channel group l/16) builds its 32 K values from 3-4
-//        byte-permuted windows of its packed row: one and-or puts a code pair
-//        into the mantissas of two fp16 numbers 2^(10-o) + c (o = the code's
-//        bit offset in the window), one packed fma with (s, -2^(10-o) s)
-//        gives round16(c*s) exactly, one packed add gives round16(. + z): the
-//        reference's fp16 dequant bit for bit.  The per-channel (s, n, z)
-//        pairs of a block are prepared once per wave in LDS.
-//   softmax: online, log2 domain, lazy rescale (threshold 2^8); probabilities
-//        enter PV as fp16 scaled by 2^7.
-//   PV:  O^T[16 chunks x 16 rows] += V^T . P^T, 8 x v_mfma_f32_16x16x16_f16.
-//        Lane (chunk l%16 of 8 channels, tokens 4(l/16)..+3) pairs two tokens
-//        per dword with byte permutes and shifts; one and-or and one packed
-//        fma give round16(c*s) with the token's scale of its group.  The
-//        zero-points enter through one more MFMA per tile that accumulates
-//        sum_t P * z(token, group), added to every channel of the group at
-//        the end (so V skips the second fp16 rounding of the reference's
-//        dequant: the output stays within the attention tolerance).
-// The 4 waves merge in LDS and write one (m, l, acc) partial per workgroup;
-// decode_reduce_kernel merges the splits.
+// Per 32-token warm unit a wave does:
+//   QK:  S^T[16 tok x 16 rows] = K . Q^T for both 16-token halves, 4 x
+//        v_mfma_f32_16x16x32_f16 each.  Lane (token l%16, channel group l/16)
+//        builds its 32 K values from byte-permuted windows of its packed row:
+//        one and-or puts a code pair into the mantissas of two fp16 numbers
+//        2^(10-o) + c (o = the code's bit offset in the window), one packed
+//        fma with (s, -2^(10-o) s) gives round16(c*s) exactly, one packed add
+//        gives round16(. + z): the reference's fp16 dequant bit for bit.  The
+//        per-channel (s, n, z) pairs of the block are prepared per unit in
+//        LDS; the query operand is staged once per workgroup in LDS.
+//   softmax: online over the 32 tokens, log2 domain, lazy rescale (threshold
+//        2^8); probabilities enter PV as fp16 scaled by 2^7.
+//   PV:  O^T[16 chunks x 16 rows] += V^T . P^T over the 32 tokens, 8 x
+//        v_mfma_f32_16x16x32_f16.  Lane (chunk l%16 of 8 channels, tokens
+//        4(l/16)..+3 of each half) pairs two tokens per dword with byte
+//        permutes and shifts; one and-or and one packed fma give round16(c*s)
+//        with the token's scale of its group.  The zero-points enter through
+//        one more MFMA per unit that accumulates sum_t P * z(token, group),
+//        added to every channel of the group at the end (so V skips the second
+//        fp16 rounding of the reference's dequant: the output stays within the
+//        attention tolerance).
+//   OUT: the stored fp16 value of an outlier channel replaces its dequantized
+//        value: q[c] (value - dequant) joins the scores, and three exact MFMAs
+//        add sum_t P (value - dequant) to channel c's accumulator.
+// The waves merge in LDS; each workgroup writes its (m, l, acc) partial and
+// counts its arrival; the last workgroup of a (batch, kv-head, row chunk)
+// merges the partials and writes the output and the row statistics.
 //
 // A block whose scales would overflow -2^(10-o) s in fp16 (|s| >= 64) takes
 // a slower exact path: the code is recovered as an fp16 integer, then
