@@ -21,7 +21,8 @@
 //           (sum_t P z, added to every channel of the group).
 // Per column group: S^T = K . Q^T for each 16-token half (4 x 16x16x32),
 // online softmax over the 32 tokens in the log2 domain (P in fp16 x 2^7),
-// O^T += V^T . P^T over the 32 tokens (8 x 16x16x32 + 1 for the zeros).
+// O^T += V^T . P^T over the 32 tokens (8 x 16x16x32 + 1 for the zeros, whose
+// last chunk row takes ones: the row sums of P come out of the same MFMA).
 //
 // Grid: one workgroup per (batch, kv-head, token split, row tile), the
 // (batch, kv-head) index varying fastest so that consecutive workgroups --
@@ -382,9 +383,17 @@ void prefill_kernel(const PrefillParams p) {
             sm[0].acc[kk] = mfma_k32(a, pop[0], sm[0].acc[kk]);
             sm[1].acc[kk] = mfma_k32(a, pop[1], sm[1].acc[kk]);
         }
-        if (!hot) {
-            const uint32_t *za = (const uint32_t *)(vzt + lane * 4);
-            const h8 az = __builtin_bit_cast(h8, (u4){za[0], za[64], za[128], za[192]});
+        {
+            // zeros MFMA: chunk rows 0-14 take the tile's zero-points (none for hot
+            // tiles); chunk row 15 takes ones, so its output is the row sum of P (l).
+            // Chunks 12-15 share one V group, so chunk 15's zero term is chunk 12's.
+            u4 zw = {0u, 0u, 0u, 0u};
+            if (!hot) {
+                const uint32_t *za = (const uint32_t *)(vzt + lane * 4);
+                zw = (u4){za[0], za[64], za[128], za[192]};
+            }
+            if (col == 15) zw = (u4){0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
+            const h8 az = __builtin_bit_cast(h8, zw);
             sm[0].accz = mfma_k32(az, pop[0], sm[0].accz);
             sm[1].accz = mfma_k32(az, pop[1], sm[1].accz);
         }
@@ -396,7 +405,10 @@ void prefill_kernel(const PrefillParams p) {
     // ---- output (one split) or partials (decode split layout)
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
-        const float l = wsum16(sm[rg].l);
+        // l from chunk row 15 of the zeros MFMA (lanes of column group 3, element 3);
+        // that chunk's zero term is chunk 12's (element 0 of the same lanes)
+        const float l = wsum16(grp == 3 ? sm[rg].accz[3] : 0.f);
+        if (grp == 3) sm[rg].accz[3] = sm[rg].accz[0];
         const int r = r0 + 32 * wave + 16 * rg + col;
         if (r >= p.R) continue;
         if (p.nsplit == 1) {
