@@ -200,8 +200,17 @@ struct Soft {
 // row's tile max passes the bound iff one of its four lanes' maxima does.  On
 // the rare update the four lanes of a row agree on the new max through two
 // shuffles.  Returns the fp16 P^T operand (x 2^7).
+// max of three (IEEE maxNum, as fmaxf).  fmaxf over values the compiler cannot
+// prove canonical (MFMA results) costs an extra v_max per operand to quiet
+// signalling NaNs; the scores never hold one, so this takes them as they are.
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 __device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
-    const float t = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])) * sl2;
+    const float t = vmax3(vmax3(s[0], s[1], s[2]), s[3], s[3]) * sl2;
     if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
         const float tm2 = wmax16(t);
         const float mn = fmaxf(st.m2, tm2);
@@ -224,8 +233,7 @@ __device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
 // fp16 P^T operand of a 16x16x32 MFMA whose K index 8*grp + j is token
 // 4*grp + j of half 0 (j < 4) or of half 1 (j >= 4).
 __device__ __forceinline__ h8 softmax32(Soft &st, f4 s0, f4 s1, float sl2) {
-    const float t = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                          fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3]))) * sl2;
+    const float t = vmax3(vmax3(s0[0], s0[1], s0[2]), vmax3(s0[3], s1[0], s1[1]), vmax3(s1[2], s1[3], s1[3])) * sl2;
     if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
         const float tm2 = wmax16(t);
         const float mn = fmaxf(st.m2, tm2);
