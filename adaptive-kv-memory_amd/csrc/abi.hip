@@ -151,6 +151,9 @@ int check_decode(const akv_decode_args *a) {
     if (a->n_hot + nw < 1) return fail(AKV_E_SHAPE, "no tokens to attend to");
     if (!a->q || !a->out) return fail(AKV_E_INVALID, "q and out are required");
     if (!aligned16(a->q) || !aligned16(a->out)) return fail(AKV_E_ALIGN, "q/out must be 16-byte aligned");
+    // the weights are written and read back with 16-byte accesses
+    if (a->attn_weights && !aligned16(a->attn_weights))
+        return fail(AKV_E_ALIGN, "attn_weights must be 16-byte aligned");
     if (a->n_hot > 0) {
         if (!a->k_hot || !a->v_hot) return fail(AKV_E_INVALID, "k_hot/v_hot required when n_hot > 0");
         if (!aligned16(a->k_hot) || !aligned16(a->v_hot)) return fail(AKV_E_ALIGN, "hot tier must be 16-byte aligned");

@@ -100,7 +100,7 @@ typedef struct akv_decode_args {
     float sm_scale;        /* softmax scale (1/sqrt(D) in the reference) */
     akv_warm_desc warm;
     void *out;             /* [B][Hq][M][D], q dtype */
-    float *attn_weights;   /* optional [B][Hq][M][N] fp32, N = n_hot + n_warm */
+    float *attn_weights;   /* optional [B][Hq][M][N] fp32, N = n_hot + n_warm, 16-byte aligned */
     float *scores;         /* optional importance scores (n_scores,), updated in place */
     int64_t n_scores;
     float decay;

@@ -72,6 +72,14 @@ def test_decode_shape_checks():
     a.Hkv, a.D = 2, 96
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1
     assert b"head_dim" in lib.akv_last_error()
+    # weights buffers take 16-byte accesses (host-side check; pointers never dereferenced)
+    a.D = 128
+    a.q = a.out = a.k_hot = a.v_hot = 0x10000
+    a.attn_weights = 0x10004
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1
+    assert b"attn_weights must be 16-byte aligned" in lib.akv_last_error()
+    a.attn_weights = 0x10010
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0
 
 
 def _prefill_args(nat, **kw):
