@@ -840,27 +840,34 @@ __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodePar
 
 // Attention weights and importance EMA from the logit stash and the row
 // statistics written by the fast kernel's in-kernel split merge.  Workgroup =
-// 64 tokens; thread (token quad q, row lane rl) reads 4 consecutive tokens of
-// rows rl, rl + 16, ... (16-byte loads when the rows are 16-byte aligned); the
-// row statistics come with the same batch of loads.  Same arithmetic and
-// summation order as finish_kernel.
+// 4 * kWsQuads tokens; thread (token quad q, row lane rl) reads 4 consecutive
+// tokens of every (256 / kWsQuads)-th row (16-byte loads when the rows are
+// 16-byte aligned); the row statistics and the old score come with the same
+// batch of loads.
+#ifndef AKV_WS_QUADS
+#define AKV_WS_QUADS 8
+#endif
+// token quads per workgroup (4 tokens each): 8 (32 tokens, 32 row lanes) measured
+// fastest at the 32k workload (16: +0.6 us per layer, 4: +2.5 us, 32: +13 us)
+constexpr int kWsQuads = AKV_WS_QUADS;
 template <bool VEC>
 __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p) {
-    __shared__ float red[16][65];
-    const int tid = threadIdx.x, q = tid & 15, rl = tid >> 4;
+    constexpr int NQ = kWsQuads, TPW = 4 * NQ, NRL = 256 / NQ;  // tokens per workgroup, row lanes
+    constexpr int RB = NRL >= 16 ? 8 : 12;                      // rows per batch of loads
+    __shared__ float red[NRL][TPW + 1];
+    const int tid = threadIdx.x, q = tid % NQ, rl = tid / NQ;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M, N = p.N;
-    const int64_t n0 = (int64_t)blockIdx.x * 64 + 4 * q;
+    const int64_t n0 = (int64_t)blockIdx.x * TPW + 4 * q;
     // the old score is loaded with the first batch of logits, not after the reduction
-    const int64_t ns = (int64_t)blockIdx.x * 64 + tid;
-    const float sc_old = (p.scores && tid < 64 && ns < p.n_scores) ? p.scores[ns] : 0.f;
+    const int64_t ns = (int64_t)blockIdx.x * TPW + tid;
+    const float sc_old = (p.scores && tid < TPW && ns < p.n_scores) ? p.scores[ns] : 0.f;
     float imp[4] = {0.f, 0.f, 0.f, 0.f};
-    constexpr int RB = 8;  // rows per batch of loads
-    for (int64_t r0 = rl; r0 < rows; r0 += 16 * RB) {
+    for (int64_t r0 = rl; r0 < rows; r0 += NRL * RB) {
         f4 x[RB];
         float M[RB], W[RB];
 #pragma unroll
         for (int j = 0; j < RB; ++j) {
-            const int64_t r = r0 + 16 * j;
+            const int64_t r = r0 + NRL * j;
             M[j] = -INFINITY;
             W[j] = 0.f;
             x[j] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
@@ -879,7 +886,7 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
         }
 #pragma unroll
         for (int j = 0; j < RB; ++j) {
-            const int64_t r = r0 + 16 * j;
+            const int64_t r = r0 + NRL * j;
             if (r >= rows) break;
             f4 w;
 #pragma unroll
@@ -904,10 +911,10 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[rl][4 * q + i] = imp[i];
     __syncthreads();
-    if (tid < 64) {
+    if (tid < TPW) {
         float sacc = 0.f;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) sacc += red[k][tid];
+        for (int k = 0; k < NRL; ++k) sacc += red[k][tid];
         if (ns < p.n_scores) {
             // mean over (batch, head), summed over query positions
             float sc = sc_old * p.decay;
@@ -1107,7 +1114,7 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
     if (p.stash && p.split_ctr) {
         // the split kernel merged its splits and wrote the row statistics
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
-        const dim3 g((unsigned)((nmax + 63) / 64));
+        const dim3 g((unsigned)((nmax + 4 * kWsQuads - 1) / (4 * kWsQuads)));
         if (p.N % 4 == 0) hipLaunchKernelGGL(weights_stats_kernel<true>, g, dim3(256), 0, s, p);
         else hipLaunchKernelGGL(weights_stats_kernel<false>, g, dim3(256), 0, s, p);
         return hipGetLastError();
