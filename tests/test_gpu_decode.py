@@ -118,6 +118,22 @@ def test_fast_outlier_channels(bk, bv, of):
     assert_close_attn(out, ref)
 
 
+def test_fast_outliers_weights_and_importance():
+    """Attention weights and the importance EMA through the outlier variant (the
+    corrected scores are what the logit stash holds)."""
+    announce("decode fast path outliers + weights + importance")
+    q, kh, vh, w, kd, vd = _case(2, 8, 4, 128, 48, 500, 4, 2, of=0.02, outl=0, heavy=4, seed=9)
+    N = kh.shape[2] + w["N"]
+    s0 = np.random.default_rng(4).random(N).astype(np.float32)
+    sc = to_dev(s0)
+    out, attn = _run(q, kh, vh, w, False, scores=sc, decay=0.9, return_weights=True)
+    ref, ref_attn = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False)
+    assert_close_attn(out, ref)
+    np.testing.assert_allclose(attn.cpu().numpy(), ref_attn, atol=2e-6, rtol=1e-4)
+    np.testing.assert_allclose(sc.cpu().numpy(), oimp.fused_importance_update(ref_attn, s0, 0.9),
+                               rtol=1e-5, atol=1e-6)
+
+
 def test_fast_outliers_nonzero_meta():
     """The stored values replace whatever the codes at an outlier channel
     dequantize to: with the channel's K scale / zero made non-zero and random
