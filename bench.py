@@ -109,8 +109,8 @@ def main():
     ap.add_argument("--bits", type=int, default=3, help="demotion workload: code width (2, 3 or 4)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU; the warm-tier path has no multi-GPU leg "
-                                   "(see DESIGN.md for how it would shard)", "n_gpus": args.gpus}))
+        print(json.dumps({"error": "one GPU only: the warm-tier path has no multi-GPU leg (a (batch, kv-head) "
+                                   "shard per GPU needs no communication)", "n_gpus": args.gpus}))
         sys.exit(2)
 
     import torch
