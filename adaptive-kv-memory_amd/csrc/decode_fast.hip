@@ -143,12 +143,16 @@ __device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, i
 
 // Logits of 4 consecutive tokens of one row (log2 domain): one 16-byte store when
 // all 4 are valid and the row offset is 16-byte aligned (vec), else one per token.
+// The 16-byte stores write through to the device coherence point (cache policy
+// sc1): the stash leaves during the kernel instead of in the end-of-kernel L2
+// write-back (measured 0.35 us per layer faster at the 32k workload).
 __device__ __forceinline__ void stash4(const DecodeParams &p, int64_t strow, int row_valid, int64_t n0, f4 s,
-                                       float sl2, int nvalid, bool vec) {
+                                       float sl2, int nvalid, bool vec, __amdgpu_buffer_rsrc_t srs, int64_t sbase) {
     if (!p.stash || !row_valid) return;
     float *dst = p.stash + strow + n0;
     if (vec && nvalid >= 4) {
-        *(f4 *)dst = s * sl2;
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, s * sl2), srs, (int)((strow + n0 - sbase) * 4),
+                                               0, 16);
         return;
     }
 #pragma unroll
@@ -260,7 +264,13 @@ void decode_fast_kernel(const DecodeParams p) {
     const int64_t warm_base = p.hot_first ? p.n_hot : 0;  // logical position of warm token 0
     const int64_t hot_base = p.hot_first ? 0 : p.n_warm;
     // the stash rows are N floats apart: 16-byte stores need N and the segment base divisible by 4
-    const bool st_vec_w = p.N % 4 == 0 && warm_base % 4 == 0, st_vec_h = p.N % 4 == 0 && hot_base % 4 == 0;
+    // the stash rows of this (batch, kv-head) as one buffer (byte offsets below 2^31)
+    const int64_t sbase = ((int64_t)(b * p.Hq + kvh * p.g) * p.M) * p.N;
+    const bool st_buf_ok = (int64_t)p.R * p.N * 4 < ((int64_t)1 << 31);
+    const __amdgpu_buffer_rsrc_t srs =
+        make_rsrc(p.stash ? p.stash + sbase : p.stash, st_buf_ok ? (uint32_t)(p.R * p.N * 4) : 0u);
+    const bool st_vec_w = st_buf_ok && p.N % 4 == 0 && warm_base % 4 == 0,
+               st_vec_h = st_buf_ok && p.N % 4 == 0 && hot_base % 4 == 0;
 
     // this workgroup's items: warm 32-token units, then hot 16-token tiles (the
     // cheap hot items come last and even out the waves' finishing times)
@@ -549,7 +559,7 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     const int t0 = tok0 + 16 * h;
-                    stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], sl2, min(4, nw - (t0 + 4 * grp)), st_vec_w);
+                    stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], sl2, min(4, nw - (t0 + 4 * grp)), st_vec_w, srs, sbase);
                 }
             }
             const h8 pop = softmax32(stt, sc[0], sc[1], sl2);
@@ -699,7 +709,7 @@ void decode_fast_kernel(const DecodeParams p) {
                 for (int ii = 0; ii < 4; ++ii)
                     if (ii >= nvalid) sh[ii] = -INFINITY;
             }
-            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, sl2, nvalid, st_vec_h);
+            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, sl2, nvalid, st_vec_h, srs, sbase);
             hot_p = softmax16(stt, sh, sl2);
         } else {
             // ---- hot V tile: lane = (chunk col, tokens 4 grp .. +3)
