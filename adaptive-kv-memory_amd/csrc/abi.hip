@@ -60,10 +60,11 @@ bool fast_path(const akv_decode_args *a) {
     if (!(w.kind == AKV_WARM_AFFINE && a->D == 128 && w.block_t % 32 == 0 &&
           (w.group_v == 32 || w.group_v == 64 || w.group_v == 128)))
         return false;
-    // outlier channels: up to 4 per block with 32-channel V groups, when the slot fits the LDS
-    return w.n_out == 0 ||
-           (w.n_out <= 4 && w.group_v == 32 && w.k_odata && w.v_odata && w.k_oidx && w.v_oidx &&
-            akv::decode_fast_lds_bytes(akv::decode_fast_slot_bytes(w.bits_k, w.bits_v, w.group_v, w.n_out), w.n_out) <= 160 * 1024);
+    // outlier channels: up to 4 per block with 32-channel V groups; the ring must fit the LDS
+    if (w.n_out != 0 && !(w.n_out <= 4 && w.group_v == 32 && w.k_odata && w.v_odata && w.k_oidx && w.v_oidx))
+        return false;
+    return akv::decode_fast_lds_bytes(akv::decode_fast_slot_bytes(w.bits_k, w.bits_v, w.group_v, w.n_out), w.n_out) <=
+           160 * 1024;
 }
 
 void make_plan(const akv_decode_args *a, Plan *pl) {

@@ -855,7 +855,8 @@ static_assert(kWavesOut * (kNSOut * 4096 + kKmetaBytes) >= (2 * kWavesOut * 16 +
               "merge area overlaps the item counter");
 int64_t decode_fast_lds_bytes(int64_t slot, int n_out) {
     const int nw = n_out > 0 ? kWavesOut : kWaves, ns = n_out > 0 ? kNSOut : kNS;
-    const int64_t ring = nw * (ns * slot + kKmetaBytes) + 16 + 2 * kQldsBytes;
+    // Q operand, plus the natural-order query rows for the outlier corrections
+    const int64_t ring = nw * (ns * slot + kKmetaBytes) + 16 + (n_out > 0 ? 2 : 1) * kQldsBytes;
     const int64_t merge = (int64_t)(2 * nw * 16 + nw * 16 * kAccRow) * 4;
     return ring > merge ? ring : merge;
 }
@@ -864,9 +865,10 @@ int decode_fast_waves(int n_out) { return n_out > 0 ? kWavesOut : kWaves; }
 bool decode_fast_eligible(const DecodeParams &p, int wk) {
     if (!(wk == AKV_WARM_AFFINE && p.D == kD && p.T % kUnit == 0 && (p.Gv == 32 || p.Gv == 64 || p.Gv == 128)))
         return false;
-    // outlier channels: up to kMaxOut per block, V groups of 32 channels
-    return p.n_out == 0 || (p.n_out <= kMaxOut && p.Gv == 32 && p.k_odata && p.v_odata && p.k_oidx && p.v_oidx &&
-                            decode_fast_lds_bytes(p.slot_bytes, p.n_out) <= kLdsCap);
+    // outlier channels: up to kMaxOut per block, V groups of 32 channels; the ring must fit the LDS
+    if (p.n_out != 0 && !(p.n_out <= kMaxOut && p.Gv == 32 && p.k_odata && p.v_odata && p.k_oidx && p.v_oidx))
+        return false;
+    return p.slot_bytes > 0 && decode_fast_lds_bytes(p.slot_bytes, p.n_out) <= kLdsCap;
 }
 
 template <int BK, int BV, int NG, int NS, bool OUT>
