@@ -31,7 +31,9 @@ __device__ __forceinline__ u4 rsrc4(const void *base, uint32_t bytes) {
 // resource range arrive as zeros.  Written as one asm block so the compiler
 // can neither merge two of them under divergent control flow nor change how
 // many are issued (the vmcnt waits count them); M0 is restored afterwards.
-// M0 is written several instructions before the load that reads it.
+// M0 is written several instructions before the load that reads it.  The
+// loads are non-temporal (each byte is read once; measured 0.5 us per layer
+// faster at the 32k decode workload than the default policy).
 __device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff, uint64_t mask) {
     uint64_t saved;
     uint32_t saved_m0;
@@ -41,7 +43,7 @@ __device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint
         "s_mov_b64 %[sv], exec\n\t"
         "s_and_b64 exec, exec, %[mask]\n\t"
         "s_nop 0\n\t"
-        "buffer_load_dwordx4 %[voff], %[rsrc], %[soff] offen lds\n\t"
+        "buffer_load_dwordx4 %[voff], %[rsrc], %[soff] offen nt lds\n\t"
         "s_mov_b64 exec, %[sv]\n\t"
         "s_mov_b32 m0, %[sm0]"
         : [sv] "=&s"(saved), [sm0] "=&s"(saved_m0)
