@@ -876,7 +876,7 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
                 W[j] = 1.0f / p.rowstats[2 * r + 1];
                 const float *src = p.stash + r * N + n0;
                 if (VEC && n0 + 3 < N) {
-                    x[j] = *(const f4 *)src;
+                    x[j] = __builtin_nontemporal_load((const f4 *)src);  // read once
                 } else {
 #pragma unroll
                     for (int i = 0; i < 4; ++i)

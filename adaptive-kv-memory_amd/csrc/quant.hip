@@ -367,6 +367,9 @@ __device__ __forceinline__ uint32_t xor_lane(uint32_t x) { return (uint32_t)__sh
 
 }  // namespace
 
+// codes and K meta leave with non-temporal stores (written once; measured ~3%
+// faster at the 64k demotion than write-back stores)
+#define QSTORE(v, ptr) __builtin_nontemporal_store((v), (ptr))
 template <int BK, int BV, int NG>
 __global__ __launch_bounds__(256) void quant_fast_kernel(const QuantParams p) {
     constexpr int KR = 16 * BK, VR = 16 * BV, LG = 16 / NG;  // lanes (channel groups of 8) per V group
@@ -388,8 +391,9 @@ __global__ __launch_bounds__(256) void quant_fast_kernel(const QuantParams p) {
         const int64_t t = t0 + (tl < nv ? tl : 0);
         const int64_t src = p.sel ? min(max(p.sel[(int64_t)b * p.n_sel + t], (int64_t)0), p.n_src - 1) : t;
         const int64_t off = (bh * p.n_src + src) * 128 + 8 * cg;
-        if (p.k) kx[i] = *(const u4 *)((const _Float16 *)p.k + off);
-        if (p.v) vx[i] = *(const u4 *)((const _Float16 *)p.v + off);
+        // non-temporal: each row is read once (measured ~2% faster at the 64k demotion)
+        if (p.k) kx[i] = __builtin_nontemporal_load((const u4 *)((const _Float16 *)p.k + off));
+        if (p.v) vx[i] = __builtin_nontemporal_load((const u4 *)((const _Float16 *)p.v + off));
     }
 
     // ---------------------------------------------------------------- K
@@ -425,8 +429,8 @@ __global__ __launch_bounds__(256) void quant_fast_kernel(const QuantParams p) {
         }
         if (tg == 0) {
             const int64_t mi = (bh * p.nblk + blk) * 128 + 8 * cg;
-            *(u4 *)((_Float16 *)p.k_scale + mi) = (u4){sc[0], sc[1], sc[2], sc[3]};
-            *(u4 *)((_Float16 *)p.k_zero + mi) = (u4){as_u32(mn[0]), as_u32(mn[1]), as_u32(mn[2]), as_u32(mn[3])};
+            QSTORE(((u4){sc[0], sc[1], sc[2], sc[3]}), (u4 *)((_Float16 *)p.k_scale + mi));
+            QSTORE(((u4){as_u32(mn[0]), as_u32(mn[1]), as_u32(mn[2]), as_u32(mn[3])}), (u4 *)((_Float16 *)p.k_zero + mi));
         }
         const h2 hic = {(_Float16)(1024.0f + MAXV), (_Float16)(1024.0f + MAXV)};
         unsigned char *st = stage[wave][0];
@@ -443,7 +447,7 @@ __global__ __launch_bounds__(256) void quant_fast_kernel(const QuantParams p) {
         __builtin_amdgcn_wave_barrier();
         const int nbytes = nv * KR;
         unsigned char *dst = (unsigned char *)p.k_codes + (bh * p.n_sel + t0) * KR;
-        for (int o = 16 * lane; o < nbytes; o += 1024) *(u4 *)(dst + o) = *(const u4 *)(st + o);
+        for (int o = 16 * lane; o < nbytes; o += 1024) QSTORE(*(const u4 *)(st + o), (u4 *)(dst + o));
     }
 
     // ---------------------------------------------------------------- V
@@ -514,7 +518,7 @@ __global__ __launch_bounds__(256) void quant_fast_kernel(const QuantParams p) {
         __builtin_amdgcn_wave_barrier();
         const int nbytes = nv * VR;
         unsigned char *dst = (unsigned char *)p.v_codes + (bh * p.n_sel + t0) * VR;
-        for (int o = 16 * lane; o < nbytes; o += 1024) *(u4 *)(dst + o) = *(const u4 *)(st + o);
+        for (int o = 16 * lane; o < nbytes; o += 1024) QSTORE(*(const u4 *)(st + o), (u4 *)(dst + o));
         // meta: nv tokens x NG fp16 scales, then zeros (contiguous per block)
         const int mh = nv * NG;
         _Float16 *ds = (_Float16 *)p.v_scale + (bh * p.n_sel + t0) * NG;
