@@ -788,6 +788,58 @@ __device__ __forceinline__ void merge_split_row(const DecodeParams &p, int bhc, 
     }
 }
 
+// Few splits (<= 8, chunked prefill): thread = (row of the chunk, channel quad)
+// with all its split loads in flight; 256 / (D/4) rows per workgroup.
+template <int D>
+__global__ __launch_bounds__(256) void reduce_few_kernel(const DecodeParams p) {
+    constexpr int NQ = D / 4, RPW = 256 / NQ, PS = D + 4, KS = 8;
+    const int bhc = blockIdx.x;
+    const int rr = blockIdx.y * RPW + threadIdx.x / NQ, q = threadIdx.x % NQ;
+    const int chunk = bhc % p.nchunk;
+    const int64_t bh = bhc / p.nchunk;
+    const int b = (int)(bh / p.Hkv), kvh = (int)(bh % p.Hkv);
+    const int row0 = chunk * 16, nrows = min(16, p.R - row0);
+    if (rr >= nrows) return;
+    const int ns = p.nsplit;
+    const int64_t pstride = (int64_t)p.prows * PS;
+    const float *part = p.part + (bh * p.nchunk + chunk) * (int64_t)ns * pstride + rr * PS;
+    float ms[KS], ls[KS];
+    f4 xs[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        const bool in = k < ns;
+        ms[k] = in ? part[k * pstride] : -INFINITY;
+        ls[k] = in ? part[k * pstride + 1] : 0.f;
+        xs[k] = in ? *(const f4 *)(part + k * pstride + 4 + 4 * q) : (f4){0.f, 0.f, 0.f, 0.f};
+    }
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) M = fmaxf(M, ms[k]);
+    f4 o = {0.f, 0.f, 0.f, 0.f};
+    float L = 0.f;
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+        const float f = (ms[k] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(ms[k] - M);
+        o += f * xs[k];
+        L += f * ls[k];
+    }
+    const int r = row0 + rr;
+    const int h = kvh * p.g + r / p.M, m = r % p.M;
+    const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
+    if (p.out_bf16) {
+        const u2 ov = {(uint32_t)f32_to_bf16_rne(o[0] / L) | ((uint32_t)f32_to_bf16_rne(o[1] / L) << 16),
+                       (uint32_t)f32_to_bf16_rne(o[2] / L) | ((uint32_t)f32_to_bf16_rne(o[3] / L) << 16)};
+        *(u2 *)(p.out + row * D + 4 * q) = ov;
+    } else {
+        const h4 ov = {(_Float16)(o[0] / L), (_Float16)(o[1] / L), (_Float16)(o[2] / L), (_Float16)(o[3] / L)};
+        *(h4 *)(p.out + row * D + 4 * q) = ov;
+    }
+    if (q == 0 && p.rowstats) {
+        p.rowstats[2 * row] = M;
+        p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
+    }
+}
+
 template <int D>
 __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p) {
     __shared__ float sm[256 / (D / 4)], sls[256 / (D / 4)];
@@ -1094,6 +1146,13 @@ hipError_t legacy_sym_launch(const void *kz, const void *vz, int64_t n, int dt, 
 }
 
 hipError_t decode_reduce_launch(const DecodeParams &p, hipStream_t s) {
+    if (p.nsplit <= 8) {
+        const int rpw = 256 / (p.D / 4);
+        const dim3 g(p.B * p.Hkv * p.nchunk, (p.prows + rpw - 1) / rpw);
+        if (p.D == 64) hipLaunchKernelGGL(reduce_few_kernel<64>, g, dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(reduce_few_kernel<128>, g, dim3(256), 0, s, p);
+        return hipGetLastError();
+    }
     const dim3 rgrid(p.B * p.Hkv * p.nchunk, p.prows);
     if (p.D == 64) hipLaunchKernelGGL(decode_reduce_kernel<64>, rgrid, dim3(256), 0, s, p);
     else hipLaunchKernelGGL(decode_reduce_kernel<128>, rgrid, dim3(256), 0, s, p);
