@@ -590,6 +590,22 @@ void decode_fast_kernel(const DecodeParams p) {
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int pp = 0; pp < 2; ++pp) v_windows<BV>(vraw[h][2 * pp], vraw[h][2 * pp + 1], win[h][pp]);
+            // one outlier channel per block (the common case): its stored value replaces the
+            // dequantized one inside the PV operand (lanes of its chunk, MFMA kk1), so only
+            // its zero term needs a correction afterwards
+            int kk1 = -1;
+            bool gsel1 = false;
+            uint32_t ov1[4] = {0u, 0u, 0u, 0u};
+            if constexpr (OUT) {
+                if (p.n_out == 1) {
+                    const int c = __builtin_amdgcn_readfirstlane(min(max(*(const int *)(slot + L::VI), 0), kD - 1));
+                    kk1 = c & 7;
+                    gsel1 = col == (c >> 3);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        ov1[q] = *(const uint32_t *)(slot + L::VO + 2 * (16 * (q >> 1) + 4 * grp + 2 * (q & 1)));
+                }
+            }
             if (vfast) {
                 h2 vn[2][2][v_noffs<BV>()];
 #pragma unroll
@@ -610,6 +626,10 @@ void decode_fast_kernel(const DecodeParams p) {
                         const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
                         d[q] = as_u32(pk_fma(as_h2(uu), vs[h][pp], vn[h][pp][voff<BV>(kk) / v_ostep<BV>()]));
                     }
+                    if (OUT && kk == kk1) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) d[q] = gsel1 ? ov1[q] : d[q];
+                    }
                     stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
                 }
             } else {
@@ -624,6 +644,10 @@ void decode_fast_kernel(const DecodeParams p) {
                         const h2 c = as_h2(uu) - (h2){mv, mv};
                         d[q] = as_u32(c * vs[h][pp]);
                     }
+                    if (OUT && kk == kk1) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) d[q] = gsel1 ? ov1[q] : d[q];
+                    }
                     stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
                 }
             }
@@ -635,7 +659,23 @@ void decode_fast_kernel(const DecodeParams p) {
             if constexpr (OUT) {
                 const int no = p.n_out;
                 const int *vi = (const int *)(slot + L::VI);
-                for (int o = 0; o < no; ++o) {
+                if (no == 1) {  // the value went in above; take out the zero term accz added
+                    uint32_t az[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) az[q] = gsel1 ? (as_u32(vz[q >> 1][q & 1]) ^ 0x80008000u) : 0u;
+                    const h8 a3 = __builtin_bit_cast(h8, (u4){az[0], az[1], az[2], az[3]});
+                    switch (kk1) {
+                        case 0: stt.acc[0] = mfma_k32(a3, pop, stt.acc[0]); break;
+                        case 1: stt.acc[1] = mfma_k32(a3, pop, stt.acc[1]); break;
+                        case 2: stt.acc[2] = mfma_k32(a3, pop, stt.acc[2]); break;
+                        case 3: stt.acc[3] = mfma_k32(a3, pop, stt.acc[3]); break;
+                        case 4: stt.acc[4] = mfma_k32(a3, pop, stt.acc[4]); break;
+                        case 5: stt.acc[5] = mfma_k32(a3, pop, stt.acc[5]); break;
+                        case 6: stt.acc[6] = mfma_k32(a3, pop, stt.acc[6]); break;
+                        default: stt.acc[7] = mfma_k32(a3, pop, stt.acc[7]); break;
+                    }
+                }
+                for (int o = 0; o < no && no > 1; ++o) {
                     const int c = min(max(vi[2 * o], 0), kD - 1);
                     const bool gsel = col == (c >> 3);
                     uint32_t av[4], az[4];
