@@ -17,11 +17,24 @@ shared by every batch element and head):
   * ``_dequant_int4_tile`` (akv/fused_attention.py:281-317): per-head int4,
     fp32 ``u*s + z`` cast to fp16.
 
+This module is test infrastructure: only the tests, the smoke check and the
+benchmark's CPU-baseline leg use it, as the checker.
+
 Pinning: the pack/unpack vectors of tests/test_quantizer.py:88-108 and the
 8-bit MSE bound of tests/test_triton_ops.py:40-50 are restated as tests;
 dequant arithmetic is checked against float64 evaluation of the closed form
 on every code value; the symmetric branch and the uint8 wrap of code -1
 (torch prints 255 for float(-1).to(uint8)) are checked on hand-built inputs.
+``kvq_quantize`` (asymmetric, 2/4/8 bits, fp16 and fp32 inputs, ragged last
+group), ``quantize_evict`` (2/3/4/8 bits, group sizes below, at and above D)
+and ``dequant_int4_tile`` are checked against exact rational arithmetic with
+per-op round-to-nearest-even, levels enumerated for the nearest code, and a
+bit-position packer (tests/test_oracle_pinning_legacy.py), plus tie, constant
+group, active-clamp and zero-padding cases.  In ``dequant_int4_tile`` the
+fp32 product of a 4-bit code and an fp16 scale is exact, and no fp16 scale /
+zero searched (every scale below 2^-13, zeros in several binades) makes the
+fp32 sum round to fp16 differently from one rounding of the exact value, so
+the order of the reference's fp32 ops there is immaterial.
 """
 from __future__ import annotations
 
