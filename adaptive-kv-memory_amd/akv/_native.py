@@ -31,7 +31,9 @@ WARM_NONE, WARM_AFFINE, WARM_LEGACY = 0, 1, 2
 QUANT_AFFINE, QUANT_TOKEN_GROUPS, QUANT_KVQ = 0, 1, 2
 
 LIB_NAME = "libakv_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# AKV_LIB names another build of the same library (for example one compiled with
+# different tuning macros); by default the in-tree build next to this file loads.
+LIB_PATH = os.environ.get("AKV_LIB") or os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
 
 _vp = ctypes.c_void_p
 _i32 = ctypes.c_int32

@@ -321,6 +321,11 @@ int akv_decode_attn(const akv_decode_args *a, void *stream) {
         p.ks = w.k_scale; p.kz = w.k_zero; p.vs = w.v_scale; p.vz = w.v_zero;
         p.kc_row = a->D * kb / 8; p.vc_row = a->D * vb / 8;
         p.T = w.block_t; p.Gv = w.group_v;
+        p.tshift = -1;
+        if (w.block_t % 32 == 0 && pow2(w.block_t / 32)) {
+            p.tshift = 0;
+            while ((32 << p.tshift) < w.block_t) ++p.tshift;
+        }
         p.nblk = (p.n_warm + w.block_t - 1) / w.block_t;
         p.n_out = w.n_out;
         p.k_oidx = w.k_oidx; p.v_oidx = w.v_oidx;

@@ -19,6 +19,7 @@ struct DecodeParams {
     int64_t n_warm;
     int kc_row, vc_row;           // bytes per packed row
     int T, Gv;                    // affine: K token block, V channel group
+    int tshift;                   // affine: log2(T / 32) when T / 32 is a power of two, else -1
     int64_t nblk;                 // affine: K blocks per (b, kv-head)
     int n_out;                    // affine outliers per block
     const int64_t *k_oidx, *v_oidx;

@@ -95,7 +95,11 @@ struct WarmLayout {
     static constexpr int KCB = kUnit * KR, VCB = kUnit * VR;
     static constexpr int VMB = 64 * NG;               // V scale (or zero) bytes of 32 tokens
     static constexpr int NKC = (KCB + 1023) / 1024, NVC = (VCB + 1023) / 1024;
-    static constexpr int NLOAD = NKC + NVC + 4 + (OUT ? 4 : 0);
+    // full-lane load patterns (dma_lean) where the range sizes allow them
+    static constexpr bool LEAN_C = dma_lean_ok<KCB>() && dma_lean_ok<VCB>();
+    static constexpr bool LEAN_VM = dma_lean_ok<64 * NG>();
+    static constexpr int NLOAD = (LEAN_C ? dma_count<KCB>() + dma_count<VCB>() : NKC + NVC) + 2 +
+                                 (LEAN_VM ? 2 * dma_count<64 * NG>() : 2) + (OUT ? 4 : 0);
     static constexpr int KC = 0, VC = KCB, KS = KCB + VCB, KZ = KS + 256, VS = KZ + 256, VZ = VS + VMB;
     // outlier channels: fp16 values [token][n_out] of K and V, int64 channel indices of the block
     static constexpr int KO = VZ + VMB, VO = KO + kUnit * kMaxOut * 2, KI = VO + kUnit * kMaxOut * 2, VI = KI + 32;
@@ -108,22 +112,34 @@ struct WarmRes {
 };
 
 template <int BK, int BV, int NG, bool OUT>
-__device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T, int n_out) {
+__device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T, int tshift,
+                                           int n_out) {
     using L = WarmLayout<BK, BV, NG, OUT>;
-    const uint32_t v16 = (uint32_t)lane * 16u;
+    const uint32_t v16 = (uint32_t)lane * 16u, v4 = (uint32_t)lane * 4u;
     const uint32_t base = lds_addr(slot);
+    if constexpr (L::LEAN_C) {
+        dma_lean<L::KCB>(R.kc, base + L::KC, (uint32_t)u * L::KCB, v16, v4);
+        dma_lean<L::VCB>(R.vc, base + L::VC, (uint32_t)u * L::VCB, v16, v4);
+    } else {
 #pragma unroll
-    for (int i = 0; i < L::NKC; ++i)
-        dma16(R.kc, base + L::KC + 1024 * i, v16, (uint32_t)u * L::KCB + 1024u * i, lane_mask(L::KCB - 1024 * i));
+        for (int i = 0; i < L::NKC; ++i)
+            dma16(R.kc, base + L::KC + 1024 * i, v16, (uint32_t)u * L::KCB + 1024u * i, lane_mask(L::KCB - 1024 * i));
 #pragma unroll
-    for (int i = 0; i < L::NVC; ++i)
-        dma16(R.vc, base + L::VC + 1024 * i, v16, (uint32_t)u * L::VCB + 1024u * i, lane_mask(L::VCB - 1024 * i));
-    const uint32_t blk = (uint32_t)((u * kUnit) / T);
+        for (int i = 0; i < L::NVC; ++i)
+            dma16(R.vc, base + L::VC + 1024 * i, v16, (uint32_t)u * L::VCB + 1024u * i, lane_mask(L::VCB - 1024 * i));
+    }
+    // K block of the unit: T / 32 units per block (a shift when that is a power of two)
+    const uint32_t blk = tshift >= 0 ? (uint32_t)u >> tshift : (uint32_t)((u * kUnit) / T);
     const uint32_t kmrow = blk * 256u;
-    dma16(R.ks, base + L::KS, v16, kmrow, 0xFFFFull);
-    dma16(R.kz, base + L::KZ, v16, kmrow, 0xFFFFull);
-    dma16(R.vs, base + L::VS, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
-    dma16(R.vz, base + L::VZ, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+    dma_lean<256>(R.ks, base + L::KS, kmrow, v16, v4);
+    dma_lean<256>(R.kz, base + L::KZ, kmrow, v16, v4);
+    if constexpr (L::LEAN_VM) {
+        dma_lean<64 * NG>(R.vs, base + L::VS, (uint32_t)u * (uint32_t)L::VMB, v16, v4);
+        dma_lean<64 * NG>(R.vz, base + L::VZ, (uint32_t)u * (uint32_t)L::VMB, v16, v4);
+    } else {
+        dma16(R.vs, base + L::VS, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+        dma16(R.vz, base + L::VZ, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+    }
     if (OUT) {
         const uint32_t ob = (uint32_t)(kUnit * n_out * 2);  // 64 n_out bytes of values per unit
         const uint64_t im = lane_mask((n_out * 8 + 15) & ~15);
@@ -135,10 +151,8 @@ __device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot
 }
 
 __device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, int tile) {
-    const uint32_t base = lds_addr(slot);
-#pragma unroll
-    for (int i = 0; i < kHotLoads; ++i)
-        dma16(r, base + 1024 * i, (uint32_t)lane * 16u, (uint32_t)tile * 4096u + 1024u * i, ~0ull);
+    static_assert(dma_count<4096>() == kHotLoads, "hot tile loads");
+    dma_lean<4096>(r, lds_addr(slot), (uint32_t)tile * 4096u, (uint32_t)lane * 16u, (uint32_t)lane * 4u);
 }
 
 // Logits of 4 consecutive tokens of one row (log2 domain): one 16-byte store when
@@ -333,7 +347,7 @@ void decode_fast_kernel(const DecodeParams p) {
         }
     };
     auto issue = [&](int k, int id, unsigned char *slot) {
-        if (k == kWarm) issue_warm<BK, BV, NG, OUT>(R, slot, lane, id, p.T, p.n_out);
+        if (k == kWarm) issue_warm<BK, BV, NG, OUT>(R, slot, lane, id, p.T, p.tshift, p.n_out);
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };

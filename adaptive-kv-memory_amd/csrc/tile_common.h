@@ -50,6 +50,55 @@ __device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint
         : [lds] "s"(lds), [mask] "s"(mask), [voff] "v"(voff), [rsrc] "s"(rsrc), [soff] "s"(soff)
         : "memory");
 }
+// One contiguous range of BYTES bytes (buffer offset soff) into LDS [lds, lds + BYTES)
+// with every lane active: 1 KiB pieces as 16-byte loads, 256-byte pieces as 4-byte
+// loads.  The instruction's immediate offset advances the buffer and the LDS address
+// alike, so one M0 value (set once, restored at the end of the block) serves the whole
+// range.  v16 = lane * 16, v4 = lane * 4.  dma_count<BYTES>() is the number of loads
+// issued (the vmcnt accounting of the callers counts them).
+template <int BYTES>
+__host__ __device__ constexpr bool dma_lean_ok() {
+    return BYTES == 256 || BYTES == 512 || BYTES == 1024 || BYTES == 1536 || BYTES == 2048 || BYTES == 3072 ||
+           BYTES == 4096;
+}
+template <int BYTES>
+__host__ __device__ constexpr int dma_count() {
+    return BYTES / 1024 + (BYTES % 1024) / 256;
+}
+#define AKV_DMA_HEAD "s_mov_b32 %[sm0], m0\n\ts_mov_b32 m0, %[lds]\n\ts_nop 0\n\t"
+#define AKV_DMA_X4(off) "buffer_load_dwordx4 %[v16], %[rsrc], %[soff] offen offset:" #off " nt lds\n\t"
+#define AKV_DMA_X1(off) "buffer_load_dword %[v4], %[rsrc], %[soff] offen offset:" #off " nt lds\n\t"
+#define AKV_DMA_TAIL "s_mov_b32 m0, %[sm0]"
+#define AKV_DMA_ARGS                                                                           \
+    : [sm0] "=&s"(saved_m0)                                                                    \
+    : [lds] "s"(lds), [v16] "v"(v16), [v4] "v"(v4), [rsrc] "s"(rsrc), [soff] "s"(soff) : "memory"
+template <int BYTES>
+__device__ __forceinline__ void dma_lean(u4 rsrc, uint32_t lds, uint32_t soff, uint32_t v16, uint32_t v4) {
+    static_assert(dma_lean_ok<BYTES>(), "range size without a full-lane load pattern");
+    uint32_t saved_m0;
+    if constexpr (BYTES == 256) {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X1(0) AKV_DMA_TAIL AKV_DMA_ARGS);
+    } else if constexpr (BYTES == 512) {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X1(0) AKV_DMA_X1(256) AKV_DMA_TAIL AKV_DMA_ARGS);
+    } else if constexpr (BYTES == 1024) {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X4(0) AKV_DMA_TAIL AKV_DMA_ARGS);
+    } else if constexpr (BYTES == 1536) {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X4(0) AKV_DMA_X1(1024) AKV_DMA_X1(1280) AKV_DMA_TAIL AKV_DMA_ARGS);
+    } else if constexpr (BYTES == 2048) {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X4(0) AKV_DMA_X4(1024) AKV_DMA_TAIL AKV_DMA_ARGS);
+    } else if constexpr (BYTES == 3072) {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X4(0) AKV_DMA_X4(1024) AKV_DMA_X4(2048) AKV_DMA_TAIL AKV_DMA_ARGS);
+    } else {
+        asm volatile(AKV_DMA_HEAD AKV_DMA_X4(0) AKV_DMA_X4(1024) AKV_DMA_X4(2048) AKV_DMA_X4(3072) AKV_DMA_TAIL
+                         AKV_DMA_ARGS);
+    }
+}
+#undef AKV_DMA_HEAD
+#undef AKV_DMA_X4
+#undef AKV_DMA_X1
+#undef AKV_DMA_TAIL
+#undef AKV_DMA_ARGS
+
 __device__ __forceinline__ uint64_t lane_mask(int bytes) {  // lanes covering `bytes` (>= 16)
     return bytes >= 1024 ? ~0ull : ((1ull << (bytes >> 4)) - 1ull);
 }
