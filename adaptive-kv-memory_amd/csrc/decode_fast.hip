@@ -411,20 +411,16 @@ void decode_fast_kernel(const DecodeParams p) {
 
     h4 hot_p = {};  // P of the hot tile whose K half was just processed
     int head = 0;  // ring slot of the oldest queue entry
-    for (;;) {
-        const int k = qk[0];
-        const int id = qi[0];
-        if (k == kNone) break;
-        unsigned char *slot = ring + head * slot_bytes;
-        {  // wait for this slot's loads: the younger slots' loads may stay in flight
-            int nwy = 0, nhy = 0;
+    // Wait for the head slot's loads (the younger slots' loads may stay in flight);
+    // on the first item, issue the other slots once the first has landed.
+    auto wait_head = [&]() {
+        int nwy = 0, nhy = 0;
 #pragma unroll
-            for (int i = 1; i < NS; ++i) {
-                nwy += qk[i] == kWarm;
-                nhy += qk[i] == kHotK || qk[i] == kHotV;
-            }
-            wait_younger<NLW, NLH, NS - 1>(nwy, nhy);
+        for (int i = 1; i < NS; ++i) {
+            nwy += qk[i] == kWarm;
+            nhy += qk[i] == kHotK || qk[i] == kHotV;
         }
+        wait_younger<NLW, NLH, NS - 1>(nwy, nhy);
         if (!primed) {
             primed = true;
 #pragma unroll
@@ -433,8 +429,28 @@ void decode_fast_kernel(const DecodeParams p) {
                 issue(qk[s2], qi[s2], ring + s2 * slot_bytes);
             }
         }
-
-        if (k == kWarm) {
+    };
+    // Every read of the head slot has landed: refill it with the youngest entry.
+    auto advance = [&](unsigned char *slot) {
+        wait_lgkm0();
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i + 1 < NS; ++i) {
+            qk[i] = qk[i + 1];
+            qi[i] = qi[i + 1];
+        }
+        next_unit(qk[NS - 1], qi[NS - 1]);
+        issue(qk[NS - 1], qi[NS - 1], slot);
+        head = head + 1 == NS ? 0 : head + 1;
+    };
+    // Items come from the counter in order, warm units first, so a wave's warm
+    // units all precede its hot tiles: two loops over the one ring, so that each
+    // loop body updates the accumulators along one path.
+    while (qk[0] == kWarm) {
+        const int id = qi[0];
+        unsigned char *slot = ring + head * slot_bytes;
+        wait_head();
+        {
             // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS
             //      and read back per MFMA step; the fast paths hold when no -1024 s overflows
             //      (K and V scales of the unit)
@@ -665,8 +681,10 @@ void decode_fast_kernel(const DecodeParams p) {
                     stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
                 }
             }
-            stt.accz = mfma_k32(__builtin_bit_cast(h8, (u4){as_u32(vz[0][0]), as_u32(vz[0][1]), as_u32(vz[1][0]), as_u32(vz[1][1])}),
-                                pop, stt.accz);
+            {
+                const h8 az8 = __builtin_bit_cast(h8, (u4){as_u32(vz[0][0]), as_u32(vz[0][1]), as_u32(vz[1][0]), as_u32(vz[1][1])});
+                stt.accz = mfma_k32(az8, pop, stt.accz);
+            }
             // ---- outlier channels of V: channel c of chunk c/8 took round16(code s) + z
             //      (z through accz); three exact MFMAs add sum_t P (value - round16(code s) - z)
             //      to its accumulator, in the lanes of that chunk only
@@ -738,7 +756,15 @@ void decode_fast_kernel(const DecodeParams p) {
                     }
                 }
             }
-        } else if (k == kHotK) {
+        }
+        advance(slot);
+    }
+    while (qk[0] != kNone) {
+        const int k = qk[0];
+        const int id = qi[0];
+        unsigned char *slot = ring + head * slot_bytes;
+        wait_head();
+        if (k == kHotK) {
             // ---- hot K tile: 16 tokens x 256 B; lane = (token col, 32 channels of group grp)
             uint32_t nat[16], pairs[16];
 #pragma unroll
@@ -778,18 +804,7 @@ void decode_fast_kernel(const DecodeParams p) {
                 stt.acc[kk] = mfma_k16(__builtin_bit_cast(h4, (u2){lo, hi}), hot_p, stt.acc[kk]);
             }
         }
-
-        // ---- every read of this slot has landed: refill it with the youngest entry
-        wait_lgkm0();
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int i = 0; i + 1 < NS; ++i) {
-            qk[i] = qk[i + 1];
-            qi[i] = qi[i + 1];
-        }
-        next_unit(qk[NS - 1], qi[NS - 1]);
-        issue(qk[NS - 1], qi[NS - 1], slot);
-        head = head + 1 == NS ? 0 : head + 1;
+        advance(slot);
     }
 
     // ---- merge the waves (the ring memory is reused): every wave rescales its
