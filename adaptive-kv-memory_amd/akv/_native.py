@@ -27,6 +27,9 @@ AKV_E_HIP = -8
 AKV_E_ABI = -9
 
 DT_F16, DT_BF16, DT_F32 = 0, 1, 2
+# scratch limits of akv_decode_attn_noalloc (AKV_NOALLOC_* in include/akv_hip.h)
+NOALLOC_SCRATCH_BYTES = 16 << 20
+NOALLOC_COUNTER_BYTES = 64 << 10
 WARM_NONE, WARM_AFFINE, WARM_LEGACY = 0, 1, 2
 QUANT_AFFINE, QUANT_TOKEN_GROUPS, QUANT_KVQ = 0, 1, 2
 
@@ -116,7 +119,7 @@ class ImportanceArgs(ctypes.Structure):
 
 EXPORTS = (
     "akv_abi_version", "akv_last_error", "akv_struct_size",
-    "akv_decode_workspace_bytes", "akv_decode_attn",
+    "akv_decode_workspace_bytes", "akv_decode_attn", "akv_decode_attn_noalloc",
     "akv_quant_pack", "akv_dequant_unpack",
     "akv_bitpack", "akv_bitunpack", "akv_importance_update",
     "akv_prefill_workspace_bytes", "akv_prefill_attn", "akv_select_demote",
@@ -144,6 +147,8 @@ def load() -> ctypes.CDLL:
     lib.akv_decode_workspace_bytes.argtypes = [ctypes.POINTER(DecodeArgs)]
     lib.akv_decode_attn.restype = ctypes.c_int
     lib.akv_decode_attn.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    lib.akv_decode_attn_noalloc.restype = ctypes.c_int
+    lib.akv_decode_attn_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.akv_quant_pack.restype = ctypes.c_int
     lib.akv_quant_pack.argtypes = [ctypes.POINTER(QuantArgs), _vp]
     lib.akv_dequant_unpack.restype = ctypes.c_int

@@ -3,6 +3,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "akv_common.h"
@@ -288,14 +289,14 @@ int64_t akv_decode_workspace_bytes(const akv_decode_args *a) {
     return pl.total;
 }
 
-int akv_decode_attn(const akv_decode_args *a, void *stream) {
-    int rc = check_decode(a);
-    if (rc != AKV_OK) return rc;
-    Plan pl;
-    make_plan(a, &pl);
-    if (!a->workspace || a->workspace_bytes < pl.total)
-        return fail(AKV_E_WORKSPACE, "workspace of %lld bytes needed", (long long)pl.total);
-    if (!aligned16(a->workspace)) return fail(AKV_E_ALIGN, "workspace must be 16-byte aligned");
+}  // extern "C"
+
+namespace {
+
+// One decode call with its scratch carved as: the split arrival counters at `ctr`
+// (pl.ctr_bytes, zero on entry; a completed call leaves them zero again) and the
+// partials, row statistics, flags and logit stash from `ws` on.
+int decode_run(const akv_decode_args *a, const Plan &pl, char *ctr, char *ws, void *stream) {
     const akv_warm_desc &w = a->warm;
     akv::DecodeParams p{};
     p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.M = a->M; p.D = a->D;
@@ -308,9 +309,7 @@ int akv_decode_attn(const akv_decode_args *a, void *stream) {
     int kb = 4, vb = 4;
     int sym_src[2] = {0, 0};
     const int *sym_ptr = nullptr;
-    char *ws = (char *)a->workspace;
-    if (pl.fused) p.split_ctr = (uint64_t *)ws;
-    ws += pl.ctr_bytes;
+    if (pl.fused) p.split_ctr = (uint64_t *)ctr;
     p.part = (float *)ws;
     p.rowstats = (float *)(ws + pl.part_bytes);
     int *flags = (int *)(ws + pl.part_bytes + pl.rowstat_bytes);
@@ -367,6 +366,85 @@ int akv_decode_attn(const akv_decode_args *a, void *stream) {
     hipError_t e = akv::decode_launch(p, kb, vb, wk, sym_ptr, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     return ok();
+}
+
+// ---------------------------------------------------------------- scratch
+// Device scratch of the no-allocation decode entry point: one copy per GPU,
+// held until the process ends.  The first kScratchCtrBytes hold the split
+// arrival counters (8 bytes per (batch, kv-head, row chunk)) and nothing else
+// writes there; every completed call leaves them zero.  The rest takes the
+// partials, row statistics, flags and logit stash of one call.
+constexpr int64_t kScratchBytes = AKV_NOALLOC_SCRATCH_BYTES + AKV_NOALLOC_COUNTER_BYTES;
+constexpr int64_t kScratchCtrBytes = AKV_NOALLOC_COUNTER_BYTES;
+constexpr int kMaxDevices = 64;
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+char *g_scratch_ptr[kMaxDevices] = {};
+
+// The address of this device's `scratch`, found once per device (with that device
+// current) by hipGetSymbolAddress; on that first call the counter region is cleared
+// by a kernel on `stream` (no memset node, so a graph capture may contain the call).
+int scratch_base(void *stream, char **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (stream) {
+        int sdev = -1;
+        e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+        if (sdev != dev) return fail(AKV_E_INVALID, "stream belongs to device %d, but device %d is current", sdev, dev);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail(AKV_E_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!ptr) return fail(AKV_E_HIP, "hipGetSymbolAddress(scratch) returned NULL");
+        e = akv::zero_fill_launch(ptr, kScratchCtrBytes, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "scratch counter clear");
+        g_scratch_ptr[dev] = (char *)ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return AKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int akv_decode_attn(const akv_decode_args *a, void *stream) {
+    int rc = check_decode(a);
+    if (rc != AKV_OK) return rc;
+    Plan pl;
+    make_plan(a, &pl);
+    if (!a->workspace || a->workspace_bytes < pl.total)
+        return fail(AKV_E_WORKSPACE, "workspace of %lld bytes needed", (long long)pl.total);
+    if (!aligned16(a->workspace)) return fail(AKV_E_ALIGN, "workspace must be 16-byte aligned");
+    char *ws = (char *)a->workspace;
+    return decode_run(a, pl, ws, ws + pl.ctr_bytes, stream);
+}
+
+int akv_decode_attn_noalloc(const akv_decode_args *a, void *stream) {
+    int rc = check_decode(a);
+    if (rc != AKV_OK) return rc;
+    Plan pl;
+    make_plan(a, &pl);
+    if (pl.ctr_bytes > kScratchCtrBytes)
+        return fail(AKV_E_WORKSPACE, "%lld split counters exceed the %lld the no-allocation entry point holds",
+                    (long long)(pl.ctr_bytes / 8), (long long)(kScratchCtrBytes / 8));
+    if (pl.total - pl.ctr_bytes > kScratchBytes - kScratchCtrBytes)
+        return fail(AKV_E_WORKSPACE, "this call needs %lld bytes of scratch; the no-allocation entry point holds %lld",
+                    (long long)(pl.total - pl.ctr_bytes), (long long)(kScratchBytes - kScratchCtrBytes));
+    char *base = nullptr;
+    if ((rc = scratch_base(stream, &base)) != AKV_OK) return rc;
+    return decode_run(a, pl, base, base + kScratchCtrBytes, stream);
 }
 
 int akv_quant_pack(const akv_quant_args *a, void *stream) {

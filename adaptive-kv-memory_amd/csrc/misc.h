@@ -38,6 +38,8 @@ hipError_t dequant_launch(const DequantParams &p, hipStream_t s);
 hipError_t bitpack_launch(const void *codes, void *packed, int64_t rows, int dim, int bits, int prow, hipStream_t s);
 hipError_t bitunpack_launch(const void *packed, void *codes, int64_t rows, int prow, int dim, int bits, hipStream_t s);
 hipError_t importance_launch(const ImportanceParams &p, hipStream_t s);
+// bytes (a multiple of 16) of device memory at p set to zero by a kernel on s.
+hipError_t zero_fill_launch(void *p, int64_t bytes, hipStream_t s);
 // Demote selection: per row, the n smallest of `len` fp32 scores with positions [0, pf) and
 // [max(0, len - pl), len) forced to +inf, ties to the lower index, indices ascending.
 hipError_t select_launch(const float *scores, int64_t rows, int64_t len, int64_t n, int64_t pf, int64_t pl,

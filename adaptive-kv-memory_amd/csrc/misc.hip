@@ -398,6 +398,17 @@ hipError_t bitunpack_launch(const void *packed, void *codes, int64_t rows, int p
                        (const unsigned char *)packed, (unsigned char *)codes, rows, prow, dim, bits);
     return hipGetLastError();
 }
+__global__ void zero_fill_kernel(u4 *p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = (u4){0u, 0u, 0u, 0u};
+}
+hipError_t zero_fill_launch(void *p, int64_t bytes, hipStream_t s) {
+    const int64_t n16 = bytes / 16;
+    if (n16 <= 0) return hipSuccess;
+    const int64_t blocks = (n16 + 255) / 256;
+    hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, s, (u4 *)p, n16);
+    return hipGetLastError();
+}
 hipError_t importance_launch(const ImportanceParams &p, hipStream_t s) {
     if (p.n_scores == 0) return hipSuccess;
     hipLaunchKernelGGL(importance_kernel, dim3((unsigned)((p.n_scores + 255) / 256)), dim3(256), 0, s, p);

@@ -125,6 +125,24 @@ int64_t akv_decode_workspace_bytes(const akv_decode_args *args);
  * and, with `scores`, triton_ops.fused_importance_update (akv/triton_ops.py:604-650). */
 int akv_decode_attn(const akv_decode_args *args, void *stream);
 
+/* Scratch limits of akv_decode_attn_noalloc: the bytes akv_decode_workspace_bytes()
+ * reports, less the split counters, must not exceed AKV_NOALLOC_SCRATCH_BYTES, and
+ * B * Hkv * ceil(Hq/Hkv * M / 16) must not exceed AKV_NOALLOC_COUNTER_BYTES / 8. */
+#define AKV_NOALLOC_SCRATCH_BYTES (16ll << 20)
+#define AKV_NOALLOC_COUNTER_BYTES (64ll << 10)
+
+/* akv_decode_attn without the caller's workspace and without allocating: the same
+ * kernels and results, with their scratch in a device array the library holds for the
+ * rest of the process (one per GPU, AKV_NOALLOC_SCRATCH_BYTES plus the counters).
+ * `workspace` and `workspace_bytes` are ignored; a call that needs more scratch than
+ * the limits above returns AKV_E_WORKSPACE and launches nothing.  No hipMalloc, no
+ * hipFree, no memset node: it may run inside a HIP graph capture.  All calls on one
+ * GPU share that GPU's array, so calls that overlap on one GPU (different streams,
+ * or graphs replayed concurrently) race and must be serialised by the caller.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under graph capture, tight serving loops, harnesses that forbid it). */
+int akv_decode_attn_noalloc(const akv_decode_args *args, void *stream);
+
 /* -------------------------------------------------------------- quantize */
 
 /* quantize layouts */

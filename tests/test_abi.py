@@ -82,6 +82,28 @@ def test_decode_shape_checks():
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0
 
 
+def test_noalloc_limits_checked_before_any_launch():
+    """akv_decode_attn_noalloc refuses requests beyond its scratch on the host
+    (pointers are never dereferenced: the call returns before any HIP call)."""
+    from akv import _native as nat
+    lib = nat.load()
+    a = nat.DecodeArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.q_dtype = nat.DT_F16
+    a.B, a.Hq, a.Hkv, a.M, a.D = 8, 12, 2, 1, 128
+    a.q = a.out = a.k_hot = a.v_hot = 0x10000
+    a.n_hot = 65536  # logit stash 8 * 12 * 65536 * 4 B = 24 MiB > 16 MiB
+    a.scores, a.n_scores, a.decay = 0x20000, 65536, 0.9
+    a.sm_scale = 128 ** -0.5
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > nat.NOALLOC_SCRATCH_BYTES
+    assert lib.akv_decode_attn_noalloc(ctypes.byref(a), None) == nat.AKV_E_WORKSPACE
+    assert b"no-allocation entry point holds 16777216" in lib.akv_last_error()
+    # more (batch, kv-head, row chunk) counters than the counter region holds
+    a.B, a.Hq, a.Hkv, a.n_hot, a.scores, a.n_scores = 4096, 4, 4, 16, None, 0
+    assert lib.akv_decode_attn_noalloc(ctypes.byref(a), None) == nat.AKV_E_WORKSPACE
+    assert b"split counters" in lib.akv_last_error()
+
+
 def _prefill_args(nat, **kw):
     a = nat.PrefillArgs()
     a.abi_version = nat.ABI_VERSION
