@@ -13,7 +13,7 @@ from typing import Optional
 
 import torch
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 AKV_OK = 0
 AKV_E_INVALID = -1
@@ -113,7 +113,7 @@ class ImportanceArgs(ctypes.Structure):
         ("attn", _vp),
         ("B", _i64), ("H", _i64), ("M", _i64), ("N", _i64),
         ("scores", _vp), ("n_scores", _i64),
-        ("decay", ctypes.c_float), ("_pad0", _i32),
+        ("decay", ctypes.c_float), ("q_window", _i32), ("pool_kernel", _i32), ("_pad0", _i32),
     ]
 
 

@@ -43,8 +43,8 @@ class AffineQuantizer:
     # one launch quantizes K (per channel over all N) or V (per token over all D)
     def _quantize(self, x: torch.Tensor, bits: int, which: str) -> dict:
         nat.require_device(x)
-        if bits not in (2, 3, 4):
-            raise NotImplementedError(f"the MI355X quantizer packs 2/3/4-bit codes, got {bits}")
+        if bits not in (2, 3, 4, 8):
+            raise NotImplementedError(f"the MI355X quantizer takes 2/3/4-bit (packed) or 8-bit (raw) codes, got {bits}")
         lib = nat.load()
         if x.dim() != 3:
             raise ValueError("expected (H, N, D)")
@@ -91,7 +91,8 @@ class AffineQuantizer:
         if n_out:
             res["outlier_idx"] = oidx.reshape(n_out)
             res["outlier_data"] = odata[0]
-        res["codes"] = codes[0] if self.packed else bitpack.unpack(codes[0], bits, D)
+        # 8-bit codes are stored raw, packed or not (bitpack passes them through)
+        res["codes"] = codes[0] if (self.packed or bits == 8) else bitpack.unpack(codes[0], bits, D)
         return res
 
     def _dequantize(self, q: dict, which: str) -> torch.Tensor:
@@ -99,9 +100,9 @@ class AffineQuantizer:
         bits = q.get("bits", self.key_bits if which == "k" else self.value_bits)
         codes = q["codes"]
         D = q["orig_dim"]
-        if not (self.packed and bits in (2, 3, 4)):
-            if bits not in (2, 3, 4):
-                raise NotImplementedError(f"the MI355X dequant unpacks 2/3/4-bit codes, got {bits}")
+        if bits not in (2, 3, 4, 8):
+            raise NotImplementedError(f"the MI355X dequant takes 2/3/4/8-bit codes, got {bits}")
+        if not self.packed and bits != 8:
             codes = bitpack.pack(codes, bits)
         nat.require_device(codes)
         H, N = codes.shape[0], codes.shape[1]

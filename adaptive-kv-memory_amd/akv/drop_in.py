@@ -52,10 +52,16 @@ _PRESETS = {
 
 
 def select_demote_indices(importance: Optional[torch.Tensor], n_demote: int, hot_len: int,
-                          hot_budget: int) -> torch.Tensor:
-    """akv/drop_in.py:392-413 on the device (importance (hot_len,) or (B, hot_len))."""
+                          hot_budget: int, device=None) -> torch.Tensor:
+    """akv/drop_in.py:392-413 on the device (importance (hot_len,) or (B, hot_len)).
+
+    With no scores, or scores of another length, the reference falls back to FIFO
+    (``arange(n_demote)``, akv/drop_in.py:401-403); that index lands on ``device``
+    (else on the scores' device), where the gather that consumes it runs."""
     if importance is None or importance.shape[-1] != hot_len:
-        dev = importance.device if importance is not None else None
+        dev = device if device is not None else (importance.device if importance is not None else None)
+        if dev is None:
+            raise ValueError("select_demote_indices: no scores and no device for the FIFO fallback")
         return torch.arange(n_demote, device=dev)
     nat.require_device(importance)
     if not 0 <= n_demote <= hot_len:
@@ -69,6 +75,49 @@ def select_demote_indices(importance: Optional[torch.Tensor], n_demote: int, hot
     nat.check(lib.akv_select_demote(scores.data_ptr(), rows, hot_len, n_demote, protect_initial, protect_recent,
                                     idx.data_ptr(), nat.stream_of(scores)), "select_demote_indices")
     return idx
+
+
+def quantize_per_head(k: torch.Tensor, v: torch.Tensor, key_bits: int = 3, value_bits: int = 3,
+                      per_head_bits: Optional[list] = None, group_size: int = 64,
+                      outlier_fraction: float = 0.0) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """AKVLayer._quantize_per_head (akv/drop_in.py:315-374) on the device.
+
+    k, v (B, H, n, D): one AffineQuantizer call per batch element over the n tokens
+    (K per channel, V per token, outliers shared by the heads) -- or, when
+    ``per_head_bits`` names a width for each head, one call per (batch element, head)
+    with a quantizer of that width for K and V (the reference's pool keyed by bits;
+    a head-count mismatch falls back to the global widths).  Returns the dequantized
+    K, V (fp16, bit-exact with the reference) and the measured packed bytes of the
+    event (packed_layout.measure_packed_bytes).  The reference squeezes a batch of
+    one; here each batch element is its own call."""
+    from .affine_quantizer import AffineQuantConfig, AffineQuantizer
+    from .packed_layout import measure_packed_bytes
+    nat.require_device(k, v)
+    B, H, n, D = k.shape
+    out_k = torch.empty(B, H, n, D, dtype=torch.float16, device=k.device)
+    out_v = torch.empty_like(out_k)
+    packed = 0
+    if not per_head_bits or len(per_head_bits) != H:
+        qz = AffineQuantizer(AffineQuantConfig(key_bits=key_bits, value_bits=value_bits, group_size=group_size,
+                                               outlier_fraction=outlier_fraction))
+        for b in range(B):
+            qk, qv = qz.quantize_keys(k[b]), qz.quantize_values(v[b])
+            packed += measure_packed_bytes(qk, key_bits) + measure_packed_bytes(qv, value_bits)
+            out_k[b] = qz.dequantize_keys(qk)
+            out_v[b] = qz.dequantize_values(qv)
+        return out_k, out_v, packed
+    pool = {}
+    for bits in set(per_head_bits):
+        pool[bits] = AffineQuantizer(AffineQuantConfig(key_bits=bits, value_bits=bits, group_size=group_size,
+                                                       outlier_fraction=outlier_fraction))
+    for b in range(B):
+        for h, bits in enumerate(per_head_bits):
+            qz = pool[bits]
+            qk, qv = qz.quantize_keys(k[b, h:h + 1]), qz.quantize_values(v[b, h:h + 1])
+            packed += measure_packed_bytes(qk, bits) + measure_packed_bytes(qv, bits)
+            out_k[b, h] = qz.dequantize_keys(qk)[0]
+            out_v[b, h] = qz.dequantize_values(qv)[0]
+    return out_k, out_v, packed
 
 
 class AKVCache:
@@ -126,7 +175,7 @@ class AKVCache:
         keys / values: (B, H, hot_len, D) on the device; importance: (B, hot_len)
         or (hot_len,).  Returns (warm tier, selected indices (B, n_demote))."""
         B, H, hot_len, D = keys.shape
-        idx = select_demote_indices(importance, n_demote, hot_len, self.hot_budget)
+        idx = select_demote_indices(importance, n_demote, hot_len, self.hot_budget, device=keys.device)
         if idx.dim() == 1:
             idx = idx.unsqueeze(0).expand(B, -1)
         warm = quantize_kv(keys, values, self.warm_key_bits, self.warm_value_bits, self.block_t,

@@ -1,11 +1,17 @@
-"""ImportanceScorer accumulate rule on the device (akv/importance.py:19-164).
+"""ImportanceScorer on the device (akv/importance.py:19-164).
 
-The attention-sum strategies (ATTENTION_ACCUMULATION, IMPORTANCE) update a
-per-layer fp32 score vector with
-    scores[:N] = scores[:N] * decay + sum_q mean_{b,h} attn[b, h, q, :]
-through ``akv_importance_update``; the score vector grows with zeros when the
-context grows (akv/importance.py:100-108).  Strategies that are not the
-attention-sum rule are policy outside this hot path and raise.
+The per-key importance (the only pass over the attention weights) is
+    imp[n] = sum_q mean_{b,h} attn[b, h, q, n]
+computed by ``akv_importance_update``; OBSERVATION_WINDOW sums only the last
+``observation_window`` queries and average-pools imp over ``pooling_kernel``
+keys in the same kernel (akv/importance.py:96-115).  The accumulate strategies
+(ATTENTION_ACCUMULATION, IMPORTANCE, OBSERVATION_WINDOW) fold imp into the EMA
+    scores[:N] = scores[:N] * decay + imp
+in that kernel too.  The other strategies (akv/importance.py:131-151) are small
+operations on the (N,) score vector on the device: HEAVY_HITTER keeps the
+running maximum, RECENCY_WEIGHTED and FIFO replace the scores by position,
+HYBRID mixes the normalised EMA with recency.  The per-layer score vector grows
+with zeros when the context grows (akv/importance.py:117-123).
 """
 from __future__ import annotations
 
@@ -49,9 +55,11 @@ class ImportanceConfig:
 _ACCUMULATE = (ScoringStrategy.ATTENTION_ACCUMULATION, ScoringStrategy.IMPORTANCE)
 
 
-def accumulate(scores: torch.Tensor, attention_weights: torch.Tensor, decay: float) -> torch.Tensor:
+def accumulate(scores: torch.Tensor, attention_weights: torch.Tensor, decay: float,
+               q_window: int = 0, pool_kernel: int = 1) -> torch.Tensor:
     """scores (n,) fp32 on the device, in place: scores = scores*decay + sum_q mean_{b,h} attn
-    (truncated / zero-padded to n)."""
+    (truncated / zero-padded to n); q_window > 0 sums only the last q_window queries and
+    pool_kernel > 1 average-pools the per-key sum first (OBSERVATION_WINDOW)."""
     nat.require_device(scores, attention_weights)
     lib = nat.load()
     B, H, M, N = attention_weights.shape
@@ -67,6 +75,8 @@ def accumulate(scores: torch.Tensor, attention_weights: torch.Tensor, decay: flo
     a.scores = scores.data_ptr()
     a.n_scores = scores.numel()
     a.decay = float(decay)
+    a.q_window = int(q_window)
+    a.pool_kernel = int(pool_kernel)
     nat.check(lib.akv_importance_update(ctypes.byref(a), nat.stream_of(scores)), "importance update")
     return scores
 
@@ -90,11 +100,11 @@ class ImportanceScorer:
         return self._step_count
 
     def update(self, attention_weights: Optional[torch.Tensor], layer_idx: int):
+        """akv/importance.py:73-156: fold one step's attention weights (B, H, M, N) into
+        the layer's scores."""
         if attention_weights is None:
             return
         cfg = self.config
-        if cfg.strategy not in _ACCUMULATE:
-            raise NotImplementedError(f"strategy {cfg.strategy} is outside the attention-sum hot path")
         kv_len = attention_weights.shape[-1]
         device = attention_weights.device
         old = self._scores.get(layer_idx)
@@ -104,8 +114,27 @@ class ImportanceScorer:
                 new[: old.shape[0]] = old.to(device)
             self._scores[layer_idx] = new
         scores = self._scores[layer_idx]
-        # only the first kv_len entries take the EMA (akv/importance.py:127-128)
-        accumulate(scores[:kv_len] if scores.shape[0] > kv_len else scores, attention_weights, cfg.decay_factor)
+        head = scores[:kv_len] if scores.shape[0] > kv_len else scores  # only the first kv_len entries change
+        st = cfg.strategy
+        if st in _ACCUMULATE:
+            accumulate(head, attention_weights, cfg.decay_factor)
+        elif st == ScoringStrategy.OBSERVATION_WINDOW:
+            accumulate(head, attention_weights, cfg.decay_factor, q_window=cfg.observation_window,
+                       pool_kernel=cfg.pooling_kernel)
+        else:
+            imp = accumulate(torch.zeros(kv_len, dtype=torch.float32, device=device), attention_weights, 0.0)
+            if st == ScoringStrategy.HEAVY_HITTER:
+                torch.maximum(head, imp, out=head)
+            elif st == ScoringStrategy.RECENCY_WEIGHTED:
+                head.copy_(torch.linspace(0, 1, kv_len, device=device))
+            elif st == ScoringStrategy.HYBRID:
+                head.mul_(cfg.decay_factor).add_(imp)
+                recency = torch.linspace(0, 1, kv_len, device=device)
+                head.copy_(cfg.attention_weight * head / head.max().clamp(min=1e-10) + cfg.recency_weight * recency)
+            elif st == ScoringStrategy.FIFO:
+                head.copy_(torch.arange(kv_len, dtype=torch.float32, device=device))
+            else:
+                raise ValueError(f"unknown strategy {st}")
         self._total_seq_len = max(self._total_seq_len, kv_len)
         self._step_count += 1
 

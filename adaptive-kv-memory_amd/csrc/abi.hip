@@ -459,8 +459,8 @@ int akv_quant_pack(const akv_quant_args *a, void *stream) {
     const bool kvq = a->layout == AKV_QUANT_KVQ;
     if (!affine && !kvq && a->layout != AKV_QUANT_TOKEN_GROUPS) return fail(AKV_E_INVALID, "unknown layout");
     for (int bits : {a->bits_k, a->bits_v}) {
-        const bool okb = affine ? (bits >= 2 && bits <= 4)
-                                : kvq ? (bits == 2 || bits == 4 || bits == 8) : (bits >= 2 && bits <= 4) || bits == 8;
+        // 8 bits: raw codes, one per byte (akv/bitpack.py:95-103 passes them through)
+        const bool okb = kvq ? (bits == 2 || bits == 4 || bits == 8) : (bits >= 2 && bits <= 4) || bits == 8;
         if (!okb) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
     }
     if (a->group_v != 32 && a->group_v != 64 && a->group_v != 128) return fail(AKV_E_UNSUPPORTED, "group_v must be 32, 64 or 128");
@@ -532,7 +532,7 @@ int akv_dequant_unpack(const akv_dequant_args *a, void *stream) {
     p.k_out = a->k_out; p.v_out = a->v_out;
     if (w.kind == AKV_WARM_AFFINE) {
         for (int bits : {w.bits_k, w.bits_v})
-            if (bits < 2 || bits > 4) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
+            if ((bits < 2 || bits > 4) && bits != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
         if (w.block_t < 1 || w.group_v < 1 || a->D % w.group_v) return fail(AKV_E_SHAPE, "bad block_t / group_v");
         if (a->out_dtype != AKV_DT_F16) return fail(AKV_E_DTYPE, "affine dequant produces float16");
         p.nbh = a->B * a->Hkv; p.Hkv = a->Hkv;
@@ -658,6 +658,11 @@ int akv_importance_update(const akv_importance_args *a, void *stream) {
     p.attn = a->attn; p.attn_dt = a->attn_dtype;
     p.B = a->B; p.H = a->H; p.M = a->M; p.N = a->N;
     p.scores = a->scores; p.n_scores = a->n_scores; p.decay = a->decay;
+    if (a->q_window < 0 || a->pool_kernel < 0 || a->pool_kernel > 64)
+        return fail(AKV_E_SHAPE, "q_window must be >= 0 and pool_kernel in [0, 64]");
+    p.m0 = (a->q_window > 0 && a->q_window < a->M) ? a->M - a->q_window : 0;
+    // the reference pools only when kv_len > kernel (akv/importance.py:111)
+    p.pool = (a->pool_kernel > 1 && a->N > a->pool_kernel) ? a->pool_kernel : 1;
     hipError_t e = akv::importance_launch(p, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "importance launch");
     return ok();

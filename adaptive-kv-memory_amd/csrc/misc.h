@@ -32,6 +32,8 @@ struct ImportanceParams {
     float *scores;
     int64_t n_scores;
     float decay;
+    int64_t m0;                   // first query row that counts (M - q_window, or 0)
+    int pool;                     // average-pool width over keys (1 = none)
 };
 
 hipError_t dequant_launch(const DequantParams &p, hipStream_t s);

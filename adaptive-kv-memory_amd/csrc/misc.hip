@@ -117,20 +117,38 @@ __global__ __launch_bounds__(256) void bitunpack_kernel(const unsigned char *pac
 }
 
 // --------------------------------------------------------------- importance
-// scores[n] = scores[n]*decay + sum_m (sum_{b,h} attn[b,h,m,n]) / (B*H)
-__global__ __launch_bounds__(256) void importance_kernel(const ImportanceParams p) {
-    const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (n >= p.n_scores) return;
+// scores[n] = scores[n]*decay + imp[n], imp[n] = sum_{m >= m0} (sum_{b,h} attn[b,h,m,n]) / (B*H);
+// with pool > 1 imp is first average-pooled over keys: (1/pool) sum_{j<pool} imp[n - pool/2 + j]
+// (zero outside [0, N)).  A workgroup owns 256 keys; with pooling it also sums the
+// pool - 1 keys of its halo into LDS, so each attention element is read about once.
+constexpr int kImpTile = 256, kImpMaxPool = 64;
+__device__ __forceinline__ float key_importance(const ImportanceParams &p, int64_t n) {
+    if (n < 0 || n >= p.N) return 0.f;
+    const float inv_bh = (float)(p.B * p.H);
     float imp = 0.f;
-    if (n < p.N) {
-        const float inv_bh = (float)(p.B * p.H);
-        for (int64_t m = 0; m < p.M; ++m) {
-            float acc = 0.f;
-            for (int64_t bh = 0; bh < p.B * p.H; ++bh)
-                acc += load_as_f32(p.attn, (bh * p.M + m) * p.N + n, p.attn_dt);
-            imp += acc / inv_bh;
-        }
+    for (int64_t m = p.m0; m < p.M; ++m) {
+        float acc = 0.f;
+        for (int64_t bh = 0; bh < p.B * p.H; ++bh) acc += load_as_f32(p.attn, (bh * p.M + m) * p.N + n, p.attn_dt);
+        imp += acc / inv_bh;
     }
+    return imp;
+}
+__global__ __launch_bounds__(kImpTile) void importance_kernel(const ImportanceParams p) {
+    __shared__ float halo[kImpTile + kImpMaxPool];
+    const int64_t n0 = (int64_t)blockIdx.x * kImpTile, n = n0 + threadIdx.x;
+    float imp;
+    if (p.pool > 1) {
+        const int pad = p.pool / 2, width = kImpTile + p.pool - 1;
+        for (int i = threadIdx.x; i < width; i += kImpTile) halo[i] = key_importance(p, n0 - pad + i);
+        __syncthreads();
+        imp = 0.f;
+        for (int j = 0; j < p.pool; ++j) imp += halo[threadIdx.x + j];
+        imp = imp / (float)p.pool;
+        if (n >= p.N) imp = 0.f;  // pooled output is trimmed to the N keys
+    } else {
+        imp = key_importance(p, n);
+    }
+    if (n >= p.n_scores) return;
     float s = p.scores[n] * p.decay;
     s = s + imp;
     p.scores[n] = s;

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define AKV_ABI_VERSION 1
+#define AKV_ABI_VERSION 2
 
 /* status codes */
 #define AKV_OK 0
@@ -227,12 +227,17 @@ typedef struct akv_importance_args {
     float *scores;         /* (n_scores,) fp32, updated in place */
     int64_t n_scores;
     float decay;
+    int32_t q_window;      /* > 0: only the last q_window query rows count (0 = all M rows) */
+    int32_t pool_kernel;   /* > 1 (and < N): average-pool the per-key importance over pool_kernel keys
+                              (stride 1, zero padding pool_kernel / 2, divided by pool_kernel), at most 64 */
     int32_t _pad0;
 } akv_importance_args;
 
 /* scores = scores*decay + sum_m mean_{b,h} attn (truncated / zero-padded to
  * n_scores): triton_ops.fused_importance_update (akv/triton_ops.py:604-650) and
- * ImportanceScorer.update's accumulate rule (akv/importance.py:88-92, :127-128). */
+ * ImportanceScorer.update's accumulate rule (akv/importance.py:88-92, :127-128);
+ * with q_window / pool_kernel, the OBSERVATION_WINDOW rule (akv/importance.py:96-115):
+ * the last q_window queries summed, then avg_pool1d(kernel, stride 1, padding kernel // 2). */
 int akv_importance_update(const akv_importance_args *args, void *stream);
 
 /* --------------------------------------------------------------- prefill */

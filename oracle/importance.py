@@ -7,15 +7,23 @@
 (The Triton kernel at akv/triton_ops.py:288-323 divides by M; the torch path
 and ``ImportanceScorer`` sum over queries -- the sum is followed here.)
 
-``ImportanceScorer.update`` accumulate strategies (akv/importance.py:73-164):
-ATTENTION_ACCUMULATION and IMPORTANCE apply the same EMA on the first kv_len
-scores (growing the per-layer score vector with zeros); OBSERVATION_WINDOW
-sums only the last ``observation_window`` queries and average-pools with
-``pooling_kernel`` (count_include_pad) before the EMA.
+``ImportanceScorer.update`` (akv/importance.py:73-164): ATTENTION_ACCUMULATION
+and IMPORTANCE apply the same EMA on the first kv_len scores (growing the
+per-layer score vector with zeros); OBSERVATION_WINDOW sums only the last
+``observation_window`` queries and average-pools with ``pooling_kernel``
+(count_include_pad) before the EMA; HEAVY_HITTER keeps the elementwise maximum;
+RECENCY_WEIGHTED and FIFO replace the scores by linspace(0, 1) / arange;
+HYBRID normalises the EMA by its maximum (clamped at 1e-10) and mixes in
+recency.
+
+This module is test infrastructure: only the tests, the smoke check and the
+benchmark's CPU-baseline leg use it, as the checker.
 
 Pinning: the decay KAT ``ones(32)``, zero attention, decay 0.5 -> 0.5
 (tests/test_triton_ops.py:169-174); float64 evaluation of the closed form;
-sum-over-queries vs mean checked at M > 1.
+sum-over-queries vs mean checked at M > 1; the window and pooling against a
+direct float64 loop (tests/test_oracle_pinning.py); the policy strategies
+against their closed forms evaluated elementwise in float64.
 """
 from __future__ import annotations
 
@@ -40,8 +48,8 @@ def fused_importance_update(attn: np.ndarray, scores: np.ndarray, decay: float =
 
 
 def scorer_update(scores, attn, strategy="attention_accumulation", decay=0.95,
-                  observation_window=32, pooling_kernel=7):
-    """akv/importance.py:73-164 for the accumulate strategies; returns new scores."""
+                  observation_window=32, pooling_kernel=7, attention_weight=0.7, recency_weight=0.3):
+    """akv/importance.py:73-164 (every strategy); returns new scores."""
     a = np.asarray(attn, dtype=np.float32)
     avg = a.mean(axis=(0, 1), dtype=np.float32)  # (M, N)
     key_imp = avg.sum(axis=0, dtype=np.float32)
@@ -57,13 +65,26 @@ def scorer_update(scores, attn, strategy="attention_accumulation", decay=0.95,
             L = xp.shape[0] - ks + 1
             pooled = np.array([xp[i:i + ks].sum(dtype=np.float32) for i in range(L)], np.float32) / np.float32(ks)
             key_imp = pooled[:kv_len].astype(np.float32)
-    elif strategy not in ("attention_accumulation", "importance"):
-        raise ValueError(f"strategy {strategy} is not an accumulate strategy")
     if scores is None or scores.shape[0] < kv_len:
         new = np.zeros(kv_len, np.float32)
         if scores is not None:
             new[: scores.shape[0]] = scores
         scores = new
     scores = np.array(scores, dtype=np.float32, copy=True)
-    scores[:kv_len] = (scores[:kv_len] * np.float32(decay)).astype(np.float32) + key_imp
+    head = scores[:kv_len]
+    if strategy in ("attention_accumulation", "importance", "observation_window"):  # :127-128, :146-151
+        head[:] = (head * np.float32(decay)).astype(np.float32) + key_imp
+    elif strategy == "heavy_hitter":  # :130-132
+        head[:] = np.maximum(head, key_imp)
+    elif strategy == "recency_weighted":  # :134-137
+        head[:] = np.linspace(0, 1, kv_len, dtype=np.float32)
+    elif strategy == "hybrid":  # :139-146
+        ema = (head * np.float32(decay)).astype(np.float32) + key_imp
+        rec = np.linspace(0, 1, kv_len, dtype=np.float32)
+        head[:] = (np.float32(attention_weight) * ema / max(np.float32(ema.max()), np.float32(1e-10))
+                   + np.float32(recency_weight) * rec).astype(np.float32)
+    elif strategy == "fifo":  # :148-150
+        head[:] = np.arange(kv_len, dtype=np.float32)
+    else:
+        raise ValueError(f"unknown strategy {strategy}")
     return scores

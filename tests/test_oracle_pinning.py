@@ -310,3 +310,39 @@ def test_select_demote_bruteforce():
                    key=lambda c: sum(imp[list(c)]))
         assert list(got) == sorted(best)
     assert list(osel.select_demote_indices(np.zeros(5), 3, 9, 16)) == [0, 1, 2]
+
+
+def test_scorer_policy_strategies_closed_forms():
+    """HEAVY_HITTER / RECENCY_WEIGHTED / FIFO / HYBRID of akv/importance.py:130-150,
+    element by element in float64."""
+    rng = np.random.default_rng(21)
+    a = rng.random((2, 3, 4, 9)).astype(np.float32)
+    s0 = rng.random(6).astype(np.float32)  # shorter than kv_len: grows with zeros
+    imp = a.astype(np.float64).mean(axis=(0, 1)).sum(axis=0)
+    grown = np.concatenate([s0, np.zeros(3)]).astype(np.float64)
+    hh = oimp.scorer_update(s0, a, "heavy_hitter")
+    np.testing.assert_allclose(hh, [max(g, i) for g, i in zip(grown, imp)], rtol=1e-6)
+    np.testing.assert_allclose(oimp.scorer_update(s0, a, "recency_weighted"), [i / 8 for i in range(9)], atol=1e-7)
+    np.testing.assert_array_equal(oimp.scorer_update(s0, a, "fifo"), np.arange(9, dtype=np.float32))
+    hy = oimp.scorer_update(s0, a, "hybrid", decay=0.9, attention_weight=0.7, recency_weight=0.3)
+    ema = [g * 0.9 + i for g, i in zip(grown, imp)]
+    m = max(max(ema), 1e-10)
+    np.testing.assert_allclose(hy, [0.7 * e / m + 0.3 * (k / 8) for k, e in enumerate(ema)], rtol=1e-6)
+    # a longer score vector keeps the entries past kv_len untouched
+    long = np.full(12, 5.0, np.float32)
+    np.testing.assert_array_equal(oimp.scorer_update(long, a, "fifo")[9:], 5.0)
+
+
+def test_observation_window_float64_loop():
+    """Window sum of the last W queries then avg_pool1d(ks, stride 1, pad ks//2, include pad)."""
+    rng = np.random.default_rng(22)
+    for M, N, W, ks in ((10, 40, 4, 7), (3, 30, 8, 5), (6, 12, 6, 4), (5, 6, 2, 7)):
+        a = rng.random((2, 2, M, N)).astype(np.float32)
+        got = oimp.scorer_update(None, a, "observation_window", 1.0, observation_window=W, pooling_kernel=ks)
+        avg = a.astype(np.float64).mean(axis=(0, 1))
+        w = min(W, M)
+        ki = [sum(avg[q, n] for q in range(M - w, M)) for n in range(N)]
+        if ks > 1 and N > ks:
+            pad = ks // 2
+            ki = [sum(ki[j] for j in range(n - pad, n - pad + ks) if 0 <= j < N) / ks for n in range(N)]
+        np.testing.assert_allclose(got, ki, rtol=1e-5, atol=1e-7)
