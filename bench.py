@@ -26,10 +26,11 @@ them on its own line instead.
 The roofline is taken on the attention-only replay (per layer: one launch of
 decode_fast_kernel, which also merges its splits): achieved = the op's
 algorithmic bytes / its per-layer time, from HIP events on the stream the
-kernel runs on.  `traffic` (HBM bytes per layer of
-that op) comes from the FETCH_SIZE / WRITE_SIZE counter runs recorded in
-profiles/decode_qwen_decode_32k_traffic.json, scaled by the same counters on
-a copy of known size (--calib-copy adds that copy to the run).
+kernel runs on.  `traffic` (HBM bytes per launch of each workload's dominant
+kernel) comes from the FETCH_SIZE / WRITE_SIZE counter runs recorded in
+profiles/hbm_traffic_by_workload.json, scaled by the same counters on a copy of
+known size (--calib-copy adds that copy to the run; --summarize-counters turns
+the rocprofv3 output directories into that file).
 """
 from __future__ import annotations
 
@@ -44,7 +45,7 @@ sys.path.insert(0, os.path.join(ROOT, "adaptive-kv-memory_amd"))
 
 METRIC = "decode-attn µs/layer + effective KV GB/s (% HBM peak) at 32K ctx, 1×MI355X"
 HBM_PEAK_GBPS = 8000.0
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_qwen_decode_32k_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_by_workload.json")
 CALIB_BYTES = 256 << 20  # the calibration copy reads and writes this many bytes
 
 
@@ -119,7 +120,14 @@ def main():
     ap.add_argument("--no-other-workloads", action="store_true",
                     help="headline only: skip the summaries of the other workloads")
     ap.add_argument("--bits", type=int, default=3, help="demotion workload: code width (2, 3 or 4)")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="no GPU work: summarise rocprofv3 --pmc output directories of a default run made with "
+                         "the same --steps/--warmup and --no-cpu-baseline --calib-copy")
+    ap.add_argument("--write-traffic", action="store_true",
+                    help="with --summarize-counters: record the HBM bytes per dispatch for the bench line")
     args = ap.parse_args()
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters, args.steps, args.warmup, args.write_traffic)
     if args.gpus != 1:
         print(json.dumps({"error": "one GPU only: the warm-tier path has no multi-GPU leg (a (batch, kv-head) "
                                    "shard per GPU needs no communication)", "n_gpus": args.gpus}))
@@ -187,10 +195,7 @@ def main():
     kv_gbps = nb["kv"] / (us_layer * 1e-6) / 1e9
     alg = nb["attn_total"]
     achieved = alg / (us_layer_attn * 1e-6) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_layer_attn")
+    traffic = recorded_traffic(s.name, "attention_only")
     res = {
         "metric": METRIC,
         "value": round(kv_gbps, 2),
@@ -290,7 +295,8 @@ def bench_c1(args):
                       "n_hot": s.n_hot, "n_warm": s.n_warm, "bits_k": s.bits_k, "bits_v": s.bits_v},
            "roofline": {"bound": "hbm", "achieved": round(nb["attn_total"] / (ms * 1e-3) / 1e9, 2),
                         "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                        "frac": round(nb["attn_total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "frac": round(nb["attn_total"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                        "traffic": recorded_traffic(s.name),
                         "kernel": "akv_decode_attn, 32 launches per graph replay (1.7 MB per layer: launch-bound, "
                                   "and the layer stays in the 256 MB Infinity Cache)",
                         "algorithmic_bytes_per_launch": nb["attn_total"]}}
@@ -314,6 +320,100 @@ def bench_c1(args):
                                          f"{t_cpu:.1f} s on {cores} host threads",
                                "kv_gbps": round(nb["kv"] / (us * 1e-6) / 1e9, 4)}
     return res
+
+
+def recorded_traffic(workload, phase="all"):
+    """HBM bytes per launch of the workload's dominant kernel, from the counter runs
+    summarised in TRAFFIC_FILE (None when that file has no entry)."""
+    if not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        rec = json.load(f).get("workloads", {}).get(workload, {})
+    return rec.get(phase, {}).get("hbm_bytes_per_dispatch")
+
+
+def _counter_dispatches(csv_path):
+    """rocprofv3 counter CSV -> dispatches in order: (kernel name, grid, {counter: value}, ns)."""
+    import csv
+    by_id = {}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            d = by_id.setdefault(int(r["Dispatch_Id"]), [r["Kernel_Name"], int(r["Grid_Size"]), {},
+                                                          int(r["End_Timestamp"]) - int(r["Start_Timestamp"])])
+            d[2][r["Counter_Name"]] = d[2].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    return [tuple(by_id[i]) for i in sorted(by_id)]
+
+
+def _workload_dispatches(disp, steps, warmup):
+    """Split the dispatches of one default bench run (run with --steps/--warmup as given
+    and --no-cpu-baseline --calib-copy) into the workloads' dominant kernels.  The
+    headline replays the full step (warmup + steps) x 28 times, then the attention-only
+    step as often, so its attention-only dispatches are the last of its kernel."""
+    import re
+    groups = {}
+    for name, grid, ctr, ns in disp:
+        m = re.search(r"akv::(\w+_kernel)<([^>]*)>", name)
+        key = (m.group(1) + "<" + m.group(2) + ">") if m else ("calibration copy" if "neg_kernel" in name else None)
+        if key:
+            groups.setdefault(key, []).append((grid, ctr, ns))
+    out = {}
+    L = 28
+    n_rep = (warmup + steps) * L
+    for key, ds in groups.items():
+        if key.startswith("decode_fast_kernel<3, 3,"):
+            out[("qwen_decode_32k", "attention_only")] = (key, ds[-n_rep:])
+            out[("qwen_decode_32k", "with_importance")] = (key, ds[-2 * n_rep:-n_rep])
+        elif key.startswith("decode_fast_kernel<4, 4,"):
+            out[("qwen_decode_4k", "all")] = (key, ds)
+        elif key.startswith("decode_fast_kernel<4, 2,"):
+            out[("llama7b_decode_16k", "all")] = (key, ds)
+        elif key.startswith("quant_fast_kernel<3, 3,"):
+            big = max(g for g, _, _ in ds)  # the demotion launch covers 16 x 8 heads; the headline's own build less
+            out[("llama3_demote_64k", "all")] = (key, [d for d in ds if d[0] == big])
+        elif key.startswith("prefill_kernel"):
+            out[("llama70b_prefill_128k", "all")] = (key, ds)
+        elif key == "calibration copy":
+            out[("calibration", "all")] = (key, ds[-1:])
+    return out
+
+
+def summarize_counters(run_dirs, steps, warmup, write_json):
+    """Average each workload's counters per dispatch over the counter runs in run_dirs
+    (each a rocprofv3 -d directory); FETCH_SIZE / WRITE_SIZE (KiB) are scaled by what
+    they read for the calibration copy of CALIB_BYTES (read once and written once)."""
+    import glob
+    ctr = {}
+    for d in run_dirs:
+        paths = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if len(paths) != 1:
+            raise SystemExit(f"{d}: expected one counter_collection.csv, found {len(paths)}")
+        for wk, (key, ds) in _workload_dispatches(_counter_dispatches(paths[0]), steps, warmup).items():
+            e = ctr.setdefault(wk, {"kernel": key, "dispatches": len(ds), "counters": {}, "ns": []})
+            e["ns"] += [ns for _, _, ns in ds]
+            for name in ds[0][1]:
+                e["counters"][name] = sum(c[name] for _, c, _ in ds) / len(ds)
+    cal = ctr.get(("calibration", "all"), {}).get("counters", {})
+    scale = {c: (CALIB_BYTES / 1024.0) / cal[c] for c in ("FETCH_SIZE", "WRITE_SIZE") if cal.get(c)}
+    res = {"calibration_kib": {c: cal.get(c) for c in ("FETCH_SIZE", "WRITE_SIZE")}, "calibration_bytes": CALIB_BYTES,
+           "scale": scale, "workloads": {}}
+    for (w, phase), e in sorted(ctr.items()):
+        if w == "calibration":
+            continue
+        c = e["counters"]
+        rec = {"kernel": e["kernel"], "dispatches": e["dispatches"],
+               "avg_ns_under_counters": round(sum(e["ns"]) / len(e["ns"])), "counters_per_dispatch": c}
+        if "FETCH_SIZE" in c and "WRITE_SIZE" in c and len(scale) == 2:
+            rec["hbm_bytes_per_dispatch"] = round((c["FETCH_SIZE"] * scale["FETCH_SIZE"]
+                                                   + c["WRITE_SIZE"] * scale["WRITE_SIZE"]) * 1024)
+        if c.get("SQ_WAVES"):
+            rec["per_wave"] = {k: round(v / c["SQ_WAVES"], 1) for k, v in c.items()
+                               if k.startswith("SQ_INSTS") or k.startswith("SQ_WAIT") or k.startswith("SQ_ACTIVE")}
+        res["workloads"].setdefault(w, {})[phase] = rec
+    print(json.dumps(res, indent=1))
+    if write_json:
+        with open(TRAFFIC_FILE, "w") as f:
+            json.dump(res, f, indent=1)
+            f.write("\n")
 
 
 def _event_time(fn, steps, warmup):
@@ -379,7 +479,7 @@ def bench_decode_mha(args):
                       "outlier_fraction": s.outlier_fraction, "n_out": n_out, "layers": L},
            "us_per_layer": round(us_layer, 3),
            "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": recorded_traffic(s.name),
                         "kernel": "akv_decode_attn per layer (decode_fast_kernel with outlier channels)",
                         "algorithmic_bytes_per_launch": alg, "us_per_launch": round(us_layer, 3)}}
     if not args.no_cpu_baseline:
@@ -416,7 +516,7 @@ def bench_prefill(args):
                       "context": s.N, "n_hot": s.n_hot, "n_warm": s.n_warm, "bits_k": s.bits_k, "bits_v": s.bits_v},
            "ms_per_call": round(ms, 4),
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                        "frac": round(tflops / 2500.0, 4), "traffic": None,
+                        "frac": round(tflops / 2500.0, 4), "traffic": recorded_traffic(s.name),
                         "kernel": "prefill_kernel (one launch at this shape)", "flops_per_launch": flops}}
     if not args.no_cpu_baseline:
         # oracle: dequant + fp32 attention of kv-head 0's 8 query heads at 16 positions
@@ -480,7 +580,8 @@ def bench_demote(args):
            "ms_quantize_only": round(ms_q, 4),
            "roofline": {"bound": "hbm", "achieved": round((rd + wr) / (ms_q * 1e-3) / 1e9, 2),
                         "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                        "frac": round((rd + wr) / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                        "frac": round((rd + wr) / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                        "traffic": recorded_traffic(s.name) if bits == 3 else None,
                         "kernel": "quant_fast_kernel (gather + quantize + pack, one launch)",
                         "algorithmic_bytes_per_launch": rd + wr}}
     if not args.no_cpu_baseline:
