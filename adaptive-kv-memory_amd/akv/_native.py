@@ -31,7 +31,7 @@ DT_F16, DT_BF16, DT_F32 = 0, 1, 2
 NOALLOC_SCRATCH_BYTES = 16 << 20
 NOALLOC_COUNTER_BYTES = 64 << 10
 WARM_NONE, WARM_AFFINE, WARM_LEGACY = 0, 1, 2
-QUANT_AFFINE, QUANT_TOKEN_GROUPS, QUANT_KVQ = 0, 1, 2
+QUANT_AFFINE, QUANT_TOKEN_GROUPS, QUANT_KVQ, QUANT_ARENA = 0, 1, 2, 3
 
 LIB_NAME = "libakv_hip.so"
 # AKV_LIB names another build of the same library (for example one compiled with
@@ -119,7 +119,7 @@ class ImportanceArgs(ctypes.Structure):
 
 EXPORTS = (
     "akv_abi_version", "akv_last_error", "akv_struct_size",
-    "akv_decode_workspace_bytes", "akv_decode_attn", "akv_decode_attn_noalloc",
+    "akv_decode_workspace_bytes", "akv_decode_counter_bytes", "akv_decode_attn", "akv_decode_attn_noalloc",
     "akv_quant_pack", "akv_dequant_unpack",
     "akv_bitpack", "akv_bitunpack", "akv_importance_update",
     "akv_prefill_workspace_bytes", "akv_prefill_attn", "akv_select_demote",
@@ -145,6 +145,8 @@ def load() -> ctypes.CDLL:
     lib.akv_struct_size.argtypes = [_i32]
     lib.akv_decode_workspace_bytes.restype = _i64
     lib.akv_decode_workspace_bytes.argtypes = [ctypes.POINTER(DecodeArgs)]
+    lib.akv_decode_counter_bytes.restype = _i64
+    lib.akv_decode_counter_bytes.argtypes = [ctypes.POINTER(DecodeArgs)]
     lib.akv_decode_attn.restype = ctypes.c_int
     lib.akv_decode_attn.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.akv_decode_attn_noalloc.restype = ctypes.c_int
@@ -226,13 +228,15 @@ def stream_of(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def workspace(nbytes: int, device, zero: bool = False) -> torch.Tensor:
-    """Device scratch for one call.  Decode workspaces start zeroed: their split
-    arrival counters must read zero before the first call (each call leaves them so)."""
+def workspace(nbytes: int, device, zero_prefix: int = 0) -> torch.Tensor:
+    """Device scratch for one call; its first ``zero_prefix`` bytes are zeroed (a decode
+    workspace's split arrival counters must read zero when a call starts, and each call
+    leaves them so; the rest needs no initial value)."""
     n = max(int(nbytes), 256)
-    if zero:
-        return torch.zeros(n, dtype=torch.uint8, device=device)
-    return torch.empty(n, dtype=torch.uint8, device=device)
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    if zero_prefix > 0:
+        ws[: min(int(zero_prefix), n)].zero_()
+    return ws
 
 
 def default_sm_scale(d: int) -> float:

@@ -225,7 +225,7 @@ def run_decode(q: torch.Tensor, k_hot, v_hot, desc: Optional[nat.WarmDesc], Hkv:
     nbytes = lib.akv_decode_workspace_bytes(ctypes.byref(a))
     if nbytes < 0:
         nat.check(lib.akv_decode_attn(ctypes.byref(a), None), "decode_attention")
-    ws = nat.workspace(nbytes, q.device, zero=True)
+    ws = nat.workspace(nbytes, q.device, zero_prefix=lib.akv_decode_counter_bytes(ctypes.byref(a)))
     a.workspace = ws.data_ptr()
     a.workspace_bytes = ws.numel()
     nat.check(lib.akv_decode_attn(ctypes.byref(a), nat.stream_of(q)), "decode_attention")
@@ -344,7 +344,7 @@ class DecodeCall:
         nbytes = lib.akv_decode_workspace_bytes(ctypes.byref(a))
         if nbytes < 0:
             nat.check(nat.AKV_E_INVALID, "DecodeCall: " + (lib.akv_last_error() or b"").decode())
-        self.workspace = nat.workspace(nbytes, q.device, zero=True)
+        self.workspace = nat.workspace(nbytes, q.device, zero_prefix=lib.akv_decode_counter_bytes(ctypes.byref(a)))
         a.workspace = self.workspace.data_ptr()
         a.workspace_bytes = self.workspace.numel()
         self.args = a

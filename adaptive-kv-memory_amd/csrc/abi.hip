@@ -289,6 +289,13 @@ int64_t akv_decode_workspace_bytes(const akv_decode_args *a) {
     return pl.total;
 }
 
+int64_t akv_decode_counter_bytes(const akv_decode_args *a) {
+    if (check_decode(a) != AKV_OK) return -1;
+    Plan pl;
+    make_plan(a, &pl);
+    return pl.ctr_bytes;
+}
+
 }  // extern "C"
 
 namespace {
@@ -457,10 +464,12 @@ int akv_quant_pack(const akv_quant_args *a, void *stream) {
     if (!a->sel && a->n_sel > a->n_src) return fail(AKV_E_SHAPE, "n_sel > n_src without indices");
     const bool affine = a->layout == AKV_QUANT_AFFINE;
     const bool kvq = a->layout == AKV_QUANT_KVQ;
-    if (!affine && !kvq && a->layout != AKV_QUANT_TOKEN_GROUPS) return fail(AKV_E_INVALID, "unknown layout");
+    const bool arena = a->layout == AKV_QUANT_ARENA;
+    if (!affine && !kvq && !arena && a->layout != AKV_QUANT_TOKEN_GROUPS)
+        return fail(AKV_E_INVALID, "unknown layout");
     for (int bits : {a->bits_k, a->bits_v}) {
         // 8 bits: raw codes, one per byte (akv/bitpack.py:95-103 passes them through)
-        const bool okb = kvq ? (bits == 2 || bits == 4 || bits == 8) : (bits >= 2 && bits <= 4) || bits == 8;
+        const bool okb = (kvq || arena) ? (bits == 2 || bits == 4 || bits == 8) : (bits >= 2 && bits <= 4) || bits == 8;
         if (!okb) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
     }
     if (a->group_v != 32 && a->group_v != 64 && a->group_v != 128) return fail(AKV_E_UNSUPPORTED, "group_v must be 32, 64 or 128");
@@ -479,9 +488,10 @@ int akv_quant_pack(const akv_quant_args *a, void *stream) {
     // arithmetic dtype and the scale clamp as that dtype rounds it
     p.ar_dt = kvq ? AKV_DT_F32 : a->in_dtype;
     if (kvq) p.lo = 1e-10f;
-    else if (p.ar_dt == AKV_DT_F16) p.lo = 0.0f;  // 1e-8 underflows in fp16
-    else if (p.ar_dt == AKV_DT_BF16) p.lo = __builtin_bit_cast(float, 0x322c0000u);  // bfloat16(1e-8)
-    else p.lo = 1e-8f;
+    else if (p.ar_dt == AKV_DT_F16) p.lo = 0.0f;  // 1e-8 and 1e-10 underflow in fp16
+    else if (p.ar_dt == AKV_DT_BF16)
+        p.lo = __builtin_bit_cast(float, arena ? 0x2edc0000u : 0x322c0000u);  // bfloat16(1e-10), bfloat16(1e-8)
+    else p.lo = arena ? 1e-10f : 1e-8f;
     p.symmetric = kvq && a->symmetric;
     p.k = a->k; p.v = a->v;
     p.n_src = a->n_src; p.n_sel = a->n_sel; p.sel = a->sel;

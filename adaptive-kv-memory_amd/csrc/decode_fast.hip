@@ -42,8 +42,12 @@
 //        fp16 rounding of the reference's dequant: the output stays within the
 //        attention tolerance).
 //   OUT: the stored fp16 value of an outlier channel replaces its dequantized
-//        value: q[c] (value - dequant) joins the scores, and three exact MFMAs
-//        add sum_t P (value - dequant) to channel c's accumulator.
+//        value.  K: q[c] (value - dequant) joins the scores (q[c] value alone
+//        when the channel's block meta is zero, as the quantizer leaves it).
+//        V, one outlier channel per block: the value goes into the PV operand in
+//        place of the channel's dequantized codes, and one MFMA takes the zero
+//        term the zero-point MFMA added back out; more channels: three exact
+//        MFMAs per channel add sum_t P (value - round16(code s) - z).
 // The waves merge in LDS; each workgroup writes its (m, l, acc) partial and
 // counts its arrival; the last workgroup of a (batch, kv-head, row chunk)
 // merges the partials and writes the output and the row statistics.
@@ -686,8 +690,10 @@ void decode_fast_kernel(const DecodeParams p) {
                 stt.accz = mfma_k32(az8, pop, stt.accz);
             }
             // ---- outlier channels of V: channel c of chunk c/8 took round16(code s) + z
-            //      (z through accz); three exact MFMAs add sum_t P (value - round16(code s) - z)
-            //      to its accumulator, in the lanes of that chunk only
+            //      (z through accz).  With one outlier channel its value already replaced
+            //      round16(code s) in the PV operand and one MFMA removes the z term; with more,
+            //      three exact MFMAs per channel add sum_t P (value - round16(code s) - z) to its
+            //      accumulator, in the lanes of that chunk only
             if constexpr (OUT) {
                 const int no = p.n_out;
                 const int *vi = (const int *)(slot + L::VI);

@@ -105,14 +105,24 @@ typedef struct akv_decode_args {
     int64_t n_scores;
     float decay;
     int32_t num_splits;    /* 0 = choose */
-    void *workspace;       /* device scratch, akv_decode_workspace_bytes() bytes, zero-filled before its
-                              first use; every call leaves it reusable (its split arrival counters return
-                              to zero), so one workspace serves any number of calls, not concurrent ones */
+    void *workspace;       /* device scratch of akv_decode_workspace_bytes() bytes.  Its first
+                              akv_decode_counter_bytes() bytes are the split arrival counters: they must
+                              read zero when a call starts, and every completed call leaves them zero; the
+                              rest of the workspace needs no initial value.  Reusing a workspace for a
+                              call with a larger counter region (more batch x kv-head x row-chunk pairs)
+                              needs that region zeroed again, since the earlier call kept other data
+                              there.  Calls that share a workspace must not overlap. */
     int64_t workspace_bytes;
 } akv_decode_args;
 
 /* Bytes of device workspace akv_decode_attn needs for `args`. */
 int64_t akv_decode_workspace_bytes(const akv_decode_args *args);
+
+/* Bytes at the start of that workspace holding the split arrival counters
+ * (256-byte multiple, B * Hkv * ceil(Hq/Hkv * M / 16) counters of 8 bytes); they must
+ * be zero when a call starts.  No counterpart in the reference (its Triton launches
+ * need no scratch): callers that keep one workspace per shape zero only this prefix. */
+int64_t akv_decode_counter_bytes(const akv_decode_args *args);
 
 /* Fused dequant-attention over hot fp16 + warm packed tiers (split-K, GQA),
  * optional normalised attention weights and importance EMA
@@ -160,6 +170,11 @@ int akv_decode_attn_noalloc(const akv_decode_args *args, void *stream);
  * raw; `symmetric` selects the symmetric branch (zero = 0, codes offset by
  * maxv//2).  bits 2, 4, 8. */
 #define AKV_QUANT_KVQ 2
+/* PackedKVArena.quantize_and_append (akv/packed_layout.py:106-161): the
+ * TOKEN_GROUPS arithmetic (input dtype, per-token groups along D, zero-padded)
+ * with the scale clamp at 1e-10 as the input dtype rounds it; bits 2, 4, 8.
+ * Rows are the TOKEN_GROUPS rows: the arena keeps their first D * bits / 8 bytes. */
+#define AKV_QUANT_ARENA 3
 
 typedef struct akv_quant_args {
     int32_t abi_version;
@@ -170,7 +185,7 @@ typedef struct akv_quant_args {
     int64_t n_src;
     const int64_t *sel;    /* optional [B][n_sel] token indices in [0, n_src) (NULL: tokens 0..n_sel-1) */
     int64_t n_sel;
-    int32_t bits_k, bits_v;    /* AFFINE: 2, 3, 4; TOKEN_GROUPS: 2, 3, 4, 8 */
+    int32_t bits_k, bits_v;    /* AFFINE: 2, 3, 4, 8; TOKEN_GROUPS: 2, 3, 4, 8; KVQ, ARENA: 2, 4, 8 */
     int32_t block_t, group_v;  /* T (>= 1), G (32, 64 or 128; divides D for AFFINE) */
     int32_t n_out;             /* AFFINE outlier channels per block (0 = none) */
     int32_t symmetric;         /* KVQ only: symmetric branch */

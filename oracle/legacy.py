@@ -16,6 +16,10 @@ shared by every batch element and head):
     leaves 3- and 8-bit codes unpacked.
   * ``_dequant_int4_tile`` (akv/fused_attention.py:281-317): per-head int4,
     fp32 ``u*s + z`` cast to fp16.
+  * ``PackedKVArena`` (akv/packed_layout.py:106-265): per (head, token, group)
+    quantize in the input dtype with clamp(1e-10), padding dropped before the
+    4-bit high-nibble-first / 2-bit MSB-first pack; dequant fp32 ``u*s + z``
+    (no symmetric branch) cast to the store dtype.
 
 This module is test infrastructure: only the tests, the smoke check and the
 benchmark's CPU-baseline leg use it, as the checker.
@@ -27,6 +31,8 @@ on every code value; the symmetric branch and the uint8 wrap of code -1
 (torch prints 255 for float(-1).to(uint8)) are checked on hand-built inputs.
 ``kvq_quantize`` (asymmetric, 2/4/8 bits, fp16 and fp32 inputs, ragged last
 group), ``quantize_evict`` (2/3/4/8 bits, group sizes below, at and above D)
+``arena_quantize`` (2/4/8 bits, fp16 / bf16 / fp32 inputs, constant groups where
+the 1e-10 clamp is active, D below the group size), ``arena_dequantize``
 and ``dequant_int4_tile`` are checked against exact rational arithmetic with
 per-op round-to-nearest-even, levels enumerated for the nearest code, and a
 bit-position packer (tests/test_oracle_pinning_legacy.py), plus tie, constant
@@ -193,6 +199,69 @@ def quantize_evict(keys, values, evict_mask, bits=4, group_size=128):
     kp, ks, kz = qt(keys[idx])
     vp, vs, vz = qt(np.asarray(values)[idx])
     return kp, ks, kz, vp, vs, vz
+
+
+# ------------------------------------------------------------ PackedKVArena
+
+def arena_pack(q: np.ndarray, bits: int) -> np.ndarray:
+    """PackedKVArena._pack (akv/packed_layout.py:203-229): 4-bit even channel in the
+    high nibble, 2-bit MSB first, 8-bit raw; along the last axis."""
+    q = np.asarray(q, dtype=np.uint8)
+    if bits == 4:
+        return ((q[..., 0::2] << 4) | (q[..., 1::2] & 0x0F)).astype(np.uint8)
+    if bits == 2:
+        return (((q[..., 0::4] & 3) << 6) | ((q[..., 1::4] & 3) << 4) | ((q[..., 2::4] & 3) << 2)
+                | (q[..., 3::4] & 3)).astype(np.uint8)
+    return q
+
+
+def arena_unpack(packed: np.ndarray, bits: int, target_dim: int) -> np.ndarray:
+    """PackedKVArena._unpack (akv/packed_layout.py:231-265), as float32."""
+    p = np.asarray(packed, dtype=np.uint8)
+    if bits == 4:
+        u = np.stack([(p >> 4) & 0x0F, p & 0x0F], axis=-1)
+    elif bits == 2:
+        u = np.stack([(p >> 6) & 3, (p >> 4) & 3, (p >> 2) & 3, p & 3], axis=-1)
+    else:
+        return p.astype(np.float32)
+    return u.reshape(p.shape[:-1] + (-1,)).astype(np.float32)[..., :target_dim]
+
+
+def arena_quantize(keys: np.ndarray, bits: int = 4, group_size: int = 128, dt: str = F16, store: str = F16):
+    """PackedKVArena.quantize_and_append's arithmetic (akv/packed_layout.py:127-153):
+    keys (H, N, D) in dtype ``dt`` (bf16 given as float32 holding bf16 values);
+    D zero-padded to the group size, per (head, token, group) min / max, scale =
+    (max - min) / maxv clamped at 1e-10, every op rounded to ``dt``; codes rounded
+    half-to-even and clamped to [0, maxv]; the padding dropped before packing;
+    scales and zeros cast to ``store``.  Returns (packed, scales, zeros)."""
+    if bits not in (2, 4, 8):
+        raise ValueError(f"bits must be 2, 4 or 8, got {bits}")
+    x = to_dtype(np.asarray(keys, dtype=np.float32), dt).astype(np.float32)
+    H, N, D = x.shape
+    G = (D + group_size - 1) // group_size
+    if G * group_size > D:
+        x = np.concatenate([x, np.zeros((H, N, G * group_size - D), np.float32)], axis=-1)
+    g = x.reshape(H, N, G, group_size)
+    gmin, gmax = g.min(axis=-1), g.max(axis=-1)
+    maxv = (1 << bits) - 1
+    sc = op(np.subtract, gmax, gmin, dt)
+    sc = op(np.divide, sc, np.float32(maxv), dt).astype(np.float32)
+    sc = np.where(np.isnan(sc), sc, np.maximum(sc, scalar_in(1e-10, dt)))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = op(np.divide, op(np.subtract, g, gmin[..., None], dt), sc[..., None], dt).astype(np.float32)
+    q = to_u8(np.clip(np.rint(q), 0, maxv))
+    q = q.reshape(H, N, -1)[:, :, :D]
+    return arena_pack(q, bits), to_dtype(sc, store), to_dtype(gmin, store)
+
+
+def arena_dequantize(packed, scales, zeros, bits: int, group_size: int, head_dim: int, store: str = F16):
+    """PackedKVArena.dequantize_slice (akv/packed_layout.py:163-187): fp32 u * s, then
+    + z in fp32 (two roundings), cast to the store dtype; (H, N, D)."""
+    u = arena_unpack(packed, bits, head_dim)
+    gi = np.arange(head_dim) // group_size
+    s = np.asarray(scales, dtype=np.float32)[..., gi]
+    z = np.asarray(zeros, dtype=np.float32)[..., gi]
+    return to_dtype(((u * s).astype(np.float32) + z).astype(np.float32), store)
 
 
 # ------------------------------------------------------- _dequant_int4_tile

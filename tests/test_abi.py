@@ -82,6 +82,30 @@ def test_decode_shape_checks():
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,M", [(1, 12, 2, 1), (8, 12, 2, 1), (4, 32, 32, 1), (2, 12, 2, 3), (3, 64, 2, 1),
+                                          (2, 2, 2, 9)])
+def test_decode_counter_region(B, Hq, Hkv, M):
+    """The split arrival counters are the workspace's first bytes: 8 bytes per
+    (batch, kv-head, 16-row chunk), rounded up to 256, inside the workspace."""
+    from akv import _native as nat
+    lib = nat.load()
+    a = nat.DecodeArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.q_dtype = nat.DT_F16
+    a.B, a.Hq, a.Hkv, a.M, a.D = B, Hq, Hkv, M, 128
+    a.q = a.out = a.k_hot = a.v_hot = 0x10000  # host-side planning only: never dereferenced
+    a.n_hot = 512
+    a.sm_scale = 128 ** -0.5
+    nchunk = -(-(Hq // Hkv * M) // 16)
+    expect = -(-(B * Hkv * nchunk * 8) // 256) * 256
+    assert lib.akv_decode_counter_bytes(ctypes.byref(a)) == expect
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > expect
+    a.scores, a.n_scores, a.decay = 0x20000, 512, 0.9  # the logit stash comes after the counters
+    assert lib.akv_decode_counter_bytes(ctypes.byref(a)) == expect
+    a.Hkv = 5  # invalid shapes are refused the same way as by the workspace query
+    assert lib.akv_decode_counter_bytes(ctypes.byref(a)) == -1
+
+
 def test_noalloc_limits_checked_before_any_launch():
     """akv_decode_attn_noalloc refuses requests beyond its scratch on the host
     (pointers are never dereferenced: the call returns before any HIP call)."""

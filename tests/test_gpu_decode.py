@@ -134,22 +134,35 @@ def test_fast_outliers_weights_and_importance():
                                rtol=1e-5, atol=1e-6)
 
 
-def test_fast_outliers_nonzero_meta():
+@pytest.mark.parametrize("of", [0.01, 0.02])
+def test_fast_outliers_nonzero_meta(of):
     """The stored values replace whatever the codes at an outlier channel
-    dequantize to: with the channel's K scale / zero made non-zero and random
-    codes there, the output must not change (the kernel looks the codes up)."""
-    announce("decode fast path outliers with non-zero meta at the outlier channels")
-    q, kh, vh, w, kd, vd = _case(1, 4, 2, 128, 48, 320, 4, 2, of=0.02, outl=0, heavy=2, seed=8)
+    dequantize to: with the channel's K scale / zero made non-zero, the V scale /
+    zero of its 32-channel group re-drawn, and random K and V codes everywhere,
+    the output must follow the oracle's dequant of that tier (one outlier channel
+    per block at 0.01: the V value goes into the PV operand; two at 0.02: the
+    correction MFMAs; K takes the code lookup either way)."""
+    announce(f"decode fast path outliers (fraction {of}) with non-zero meta at the outlier channels")
+    q, kh, vh, w, kd, vd = _case(1, 4, 2, 128, 48, 320, 4, 2, of=of, outl=0, heavy=2, seed=8)
+    assert w["k_oidx"].shape[-1] == (1 if of == 0.01 else 2)
     rng = np.random.default_rng(1)
     w = dict(w)
     ks, kz = w["k_scale"].copy(), w["k_zero"].copy()
+    vs, vz = w["v_scale"].copy(), w["v_zero"].copy()
+    T, G = 32, 32
     for b in range(ks.shape[0]):
         for blk in range(ks.shape[2]):
             for c in w["k_oidx"][b, blk]:
                 ks[b, :, blk, c] = rng.uniform(0.05, 0.5, ks.shape[1]).astype(np.float16)
                 kz[b, :, blk, c] = rng.uniform(-1.0, 1.0, ks.shape[1]).astype(np.float16)
-    w["k_scale"], w["k_zero"] = ks, kz
+            t0, t1 = blk * T, min((blk + 1) * T, vs.shape[2])
+            for c in w["v_oidx"][b, blk]:
+                g = int(c) // G
+                vs[b, :, t0:t1, g] = rng.uniform(0.05, 0.5, (vs.shape[1], t1 - t0)).astype(np.float16)
+                vz[b, :, t0:t1, g] = rng.uniform(-1.0, 1.0, (vs.shape[1], t1 - t0)).astype(np.float16)
+    w["k_scale"], w["k_zero"], w["v_scale"], w["v_zero"] = ks, kz, vs, vz
     w["k_codes"] = rng.integers(0, 256, w["k_codes"].shape, dtype=np.uint8)
+    w["v_codes"] = rng.integers(0, 256, w["v_codes"].shape, dtype=np.uint8)
     kd2, vd2 = oaff.dequant_kv_blocked(w)
     out = _run(q, kh, vh, w, hot_first=False)
     ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd2, vd2, hot_first=False, return_weights=False)

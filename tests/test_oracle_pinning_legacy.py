@@ -213,3 +213,95 @@ def test_quantize_evict_empty():
     keys = np.zeros((4, 64), np.float16)
     out = oleg.quantize_evict(keys, keys, np.zeros(4, bool), 4, 64)
     assert all(o.size == 0 for o in out)
+
+
+# ----------------------------------------------------------- PackedKVArena
+
+def _bf16(x: Fraction) -> Fraction:
+    from exact_fp import rne
+    return rne(x, 7, -126, 127)
+
+
+def _arena_bruteforce(x: np.ndarray, bits: int, gs: int, dt: str):
+    """quantize_and_append's arithmetic with exact rounding: every op rounded to the
+    input dtype, clamp(min=1e-10) as that dtype sees it, the nearest level to
+    rnd(rnd(x - min) / scale) (0/0 -> NaN -> 0), padding channels dropped."""
+    maxv = (1 << bits) - 1
+    rnd = {"float16": f16, "bfloat16": _bf16, "float32": f32}[dt]
+    H, N, D = x.shape
+    G = -(-D // gs)
+    lo = rnd(Fraction(1e-10))
+    codes = np.zeros((H, N, D), np.int64)
+    sc = np.zeros((H, N, G))
+    zr = np.zeros((H, N, G))
+    for h in range(H):
+        for n in range(N):
+            vals = [frac(v) for v in x[h, n]] + [Fraction(0)] * (G * gs - D)
+            for g in range(G):
+                grp = vals[g * gs:(g + 1) * gs]
+                mn, mx = min(grp), max(grp)
+                s = max(rnd(rnd(mx - mn) / maxv), lo)
+                for j, v in enumerate(grp):
+                    c = g * gs + j
+                    if c >= D:
+                        break
+                    d = rnd(v - mn)
+                    q = (float("nan") if d == 0 else float("inf")) if s == 0 else rnd(d / s)
+                    codes[h, n, c] = nearest_level(q, maxv)
+                sc[h, n, g], zr[h, n, g] = float(s), float(mn)
+    return codes, sc, zr
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("dt", ["float16", "bfloat16", "float32"])
+@pytest.mark.parametrize("D,gs", [(64, 64), (64, 32), (64, 128), (128, 128)])
+def test_arena_quantize_bruteforce(bits, dt, D, gs):
+    from oracle.fp import to_dtype
+    rng = np.random.default_rng(bits * 7 + D + gs + len(dt))
+    x = to_dtype((rng.standard_normal((2, 3, D)) * 1.7).astype(np.float32), dt).astype(np.float32)
+    x[1, 2] = np.float32(0.375)  # a constant token: scale 0 -> the 1e-10 clamp (bf16 / fp32) or NaN -> 0 (fp16)
+    p, s, z = oleg.arena_quantize(x, bits, gs, dt=dt, store="float32")
+    codes, sc, zr = _arena_bruteforce(x, bits, gs, dt)
+    per_byte = 8 // bits
+    ref = np.stack([np.stack([pack_bits_msb(codes[h, n], bits, per_byte) if bits < 8 else codes[h, n].astype(np.uint8)
+                              for n in range(x.shape[1])]) for h in range(x.shape[0])])
+    np.testing.assert_array_equal(p, ref)
+    np.testing.assert_array_equal(s.astype(np.float64), sc)
+    np.testing.assert_array_equal(z.astype(np.float64), zr)
+    assert p.shape == (2, 3, D * bits // 8)
+    if dt != "float16":
+        assert s[1, 2, 0] > 0  # the clamp took the constant token's scale off zero
+
+
+def test_arena_dequantize_closed_form():
+    """u * s + z with both ops rounded to fp32 and the sum cast to fp16, for every
+    code of every width against float64 evaluation of the same steps."""
+    rng = np.random.default_rng(3)
+    for bits in (2, 4, 8):
+        maxv = (1 << bits) - 1
+        D, gs = 64, 32
+        codes = rng.integers(0, maxv + 1, (2, 5, D))
+        codes[0, 0, : maxv + 1 if maxv < D else D] = np.arange(min(maxv + 1, D))
+        packed = oleg.arena_pack(codes.astype(np.uint8), bits)
+        s = (rng.random((2, 5, 2)) * 0.3).astype(np.float16)
+        z = (rng.standard_normal((2, 5, 2))).astype(np.float16)
+        got = oleg.arena_dequantize(packed, s, z, bits, gs, D)
+        gi = np.arange(D) // gs
+        prod = (codes * s.astype(np.float64)[..., gi]).astype(np.float32)  # exact: <= 19 significant bits
+        want = (prod.astype(np.float64) + z.astype(np.float64)[..., gi]).astype(np.float32).astype(np.float16)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(oleg.arena_unpack(packed, bits, D), codes.astype(np.float32))
+
+
+def test_arena_matches_quantize_evict_on_fp16():
+    """On fp16 inputs the two clamps (1e-8, 1e-10) both round to 0, so the arena's
+    codes, scales and zeros equal fused_quantize_evict's row by row (D a multiple of
+    the group size: no padding to drop)."""
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((3, 7, 128)) * 2).astype(np.float16)
+    for bits, gs in ((4, 128), (2, 32), (8, 64)):
+        p, s, z = oleg.arena_quantize(x, bits, gs)
+        kp, ks, kz, _, _, _ = oleg.quantize_evict(x.reshape(-1, 128), x.reshape(-1, 128), np.ones(21, bool), bits, gs)
+        np.testing.assert_array_equal(p.reshape(21, -1), kp)
+        np.testing.assert_array_equal(s.reshape(21, -1), ks)
+        np.testing.assert_array_equal(z.reshape(21, -1), kz)
