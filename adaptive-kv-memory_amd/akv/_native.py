@@ -13,7 +13,7 @@ from typing import Optional
 
 import torch
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 AKV_OK = 0
 AKV_E_INVALID = -1
@@ -104,6 +104,8 @@ class DequantArgs(ctypes.Structure):
         ("out_dtype", _i32), ("_pad0", _i32),
         ("warm", WarmDesc),
         ("k_out", _vp), ("v_out", _vp), ("workspace", _vp),
+        ("block_of_token", _vp), ("n_blocks", _i64), ("token_stride", _i64),
+        ("out_slot", _vp), ("out_tokens", _i64),
     ]
 
 

@@ -1,22 +1,26 @@
-"""AKVCache presets and the demotion primitives of the drop-in cache.
+"""The drop-in cache: AKVCache (presets, protected layers, per-layer update)
+and AKVLayer (hot fp16 tier + packed warm tier, akv/drop_in.py:169-1200).
 
 ``_PRESETS`` and the preset resolution of ``AKVCache.__init__`` follow
-akv/drop_in.py:89-124 and :910-964.  Demotion follows ``AKVLayer``:
-``select_demote_indices`` is akv/drop_in.py:392-413 (first 4 and last
-min(16, hot_budget // 4) hot tokens protected, lowest scores first, indices
-returned in ascending order) and ``demote`` gathers the selected tokens and
-quantizes them into the packed warm tier on the device (the reference's
-_quantize_per_head at akv/drop_in.py:315-374 quantizes and immediately
-dequantizes back to fp16; here the packed codes are what is kept).
+akv/drop_in.py:89-124 and :910-964.  ``select_demote_indices`` is
+akv/drop_in.py:392-413 (first 4 and last min(16, hot_budget // 4) hot tokens
+protected, lowest scores first, indices returned in ascending order).
+``AKVLayer.update`` keeps each demotion event packed (codes + scale / zero) and
+serves the chronological view from one dequant launch; the reference keeps a
+float16 working copy of the same values (_quantize_per_head at
+akv/drop_in.py:315-374 quantizes and immediately dequantizes).
+``AKVCache.demote`` quantizes a chosen token set into a warm tier of 32-token
+K blocks, for callers that drive the tiers themselves.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
 
 from . import _native as nat
-from .warm_tier import WarmTier, quantize_kv
+from .warm_tier import WarmTier, packed_row_bytes, quantize_kv
 
 _PRESETS = {
     "quality": {
@@ -120,10 +124,306 @@ def quantize_per_head(k: torch.Tensor, v: torch.Tensor, key_bits: int = 3, value
     return out_k, out_v, packed
 
 
+class _EventTier:
+    """The packed warm tier of one AKVLayer: demotion events appended in order.
+
+    Per (batch, head) the codes, V scale / zero and outlier values of every warm
+    token (``cap`` token rows), and per event the K scale / zero rows (``ecap``)
+    and per batch element its outlier channels; ``blk`` maps each warm token to
+    its event and ``pos`` to its chronological position.  Capacities double as
+    tokens arrive."""
+
+    def __init__(self, B, H, D, bits_k, bits_v, n_out, dev):
+        self.B, self.H, self.D, self.bits_k, self.bits_v, self.n_out = B, H, D, bits_k, bits_v, n_out
+        self.dev = dev
+        self.n = 0
+        self.n_events = 0
+        self.cap = self.ecap = 0
+        self.t = {}
+        self._grow(256, 16)
+
+    def _alloc(self, cap, ecap):
+        B, H, D, n_out, dev = self.B, self.H, self.D, self.n_out, self.dev
+        f16, u8 = torch.float16, torch.uint8
+        t = {
+            "kc": torch.empty(B, H, cap, packed_row_bytes(D, self.bits_k), dtype=u8, device=dev),
+            "vc": torch.empty(B, H, cap, packed_row_bytes(D, self.bits_v), dtype=u8, device=dev),
+            "vs": torch.empty(B, H, cap, 1, dtype=f16, device=dev),
+            "vz": torch.empty(B, H, cap, 1, dtype=f16, device=dev),
+            "ks": torch.empty(B, H, ecap, D, dtype=f16, device=dev),
+            "kz": torch.empty(B, H, ecap, D, dtype=f16, device=dev),
+            "blk": torch.empty(cap, dtype=torch.int32, device=dev),
+            "pos": torch.empty(cap, dtype=torch.int64, device=dev),
+        }
+        if n_out:
+            t["kod"] = torch.empty(B, H, cap, n_out, dtype=f16, device=dev)
+            t["vod"] = torch.empty(B, H, cap, n_out, dtype=f16, device=dev)
+            t["koi"] = torch.empty(B, ecap, n_out, dtype=torch.int64, device=dev)
+            t["voi"] = torch.empty(B, ecap, n_out, dtype=torch.int64, device=dev)
+        return t
+
+    _TOKEN_AXIS = {"kc": 2, "vc": 2, "vs": 2, "vz": 2, "kod": 2, "vod": 2, "blk": 0, "pos": 0}
+
+    def _grow(self, cap, ecap):
+        t = self._alloc(cap, ecap)
+        for name, old in self.t.items():
+            if name in self._TOKEN_AXIS:
+                t[name].narrow(self._TOKEN_AXIS[name], 0, self.n).copy_(old.narrow(self._TOKEN_AXIS[name], 0, self.n))
+            else:
+                ax = 2 if name in ("ks", "kz") else 1
+                t[name].narrow(ax, 0, self.n_events).copy_(old.narrow(ax, 0, self.n_events))
+        self.t, self.cap, self.ecap = t, cap, ecap
+
+    def append(self, w: WarmTier, positions: torch.Tensor):
+        """One demotion event: ``w`` holds its n tokens as a single K block."""
+        n = w.n_warm
+        if self.n + n > self.cap or self.n_events + 1 > self.ecap:
+            self._grow(max(self.cap, 2 * (self.n + n)), max(self.ecap, 2 * (self.n_events + 1)))
+        t, a, e = self.t, self.n, self.n_events
+        t["kc"][:, :, a:a + n] = w.k_codes
+        t["vc"][:, :, a:a + n] = w.v_codes
+        t["vs"][:, :, a:a + n] = w.v_scale
+        t["vz"][:, :, a:a + n] = w.v_zero
+        t["ks"][:, :, e:e + 1] = w.k_scale
+        t["kz"][:, :, e:e + 1] = w.k_zero
+        if self.n_out:
+            t["kod"][:, :, a:a + n] = w.k_odata
+            t["vod"][:, :, a:a + n] = w.v_odata
+            t["koi"][:, e:e + 1] = w.k_oidx
+            t["voi"][:, e:e + 1] = w.v_oidx
+        t["blk"][a:a + n] = e
+        t["pos"][a:a + n] = positions
+        self.n += n
+        self.n_events += 1
+
+    def resident_bytes(self) -> int:
+        """Bytes of the used extents (codes, meta, outliers, event map, positions)."""
+        total = 0
+        for name, x in self.t.items():
+            if name in self._TOKEN_AXIS:
+                total += x.narrow(self._TOKEN_AXIS[name], 0, self.n).nbytes
+            else:
+                total += x.narrow(2 if name in ("ks", "kz") else 1, 0, self.n_events).nbytes
+        return total
+
+    def dequantize_into(self, out_k: torch.Tensor, out_v: torch.Tensor, slots: bool = True):
+        """Dequantize every warm token into out_k / out_v (B, H, rows, D): at its
+        chronological position when ``slots``, else at its warm-tier index."""
+        if self.n == 0:
+            return
+        t = self.t
+        d = nat.WarmDesc()
+        d.kind = nat.WARM_AFFINE
+        d.bits_k, d.bits_v = self.bits_k, self.bits_v
+        d.n_warm = self.n
+        d.block_t = 1
+        d.group_v = self.D
+        d.n_out = self.n_out
+        d.k_codes, d.v_codes = t["kc"].data_ptr(), t["vc"].data_ptr()
+        d.k_scale, d.k_zero = t["ks"].data_ptr(), t["kz"].data_ptr()
+        d.v_scale, d.v_zero = t["vs"].data_ptr(), t["vz"].data_ptr()
+        if self.n_out:
+            d.k_oidx, d.v_oidx = t["koi"].data_ptr(), t["voi"].data_ptr()
+            d.k_odata, d.v_odata = t["kod"].data_ptr(), t["vod"].data_ptr()
+        a = nat.DequantArgs()
+        a.abi_version = nat.ABI_VERSION
+        a.B, a.Hkv, a.D = self.B, self.H, self.D
+        a.out_dtype = nat.dtype_code(out_k.dtype)
+        a.warm = d
+        a.k_out, a.v_out = out_k.data_ptr(), out_v.data_ptr()
+        a.block_of_token = t["blk"].data_ptr()
+        a.n_blocks = self.ecap
+        a.token_stride = self.cap
+        if slots:
+            a.out_slot = t["pos"].data_ptr()
+        a.out_tokens = out_k.shape[2]
+        nat.check(nat.load().akv_dequant_unpack(ctypes.byref(a), nat.stream_of(out_k)), "AKVLayer warm view")
+
+    def index_batch(self, beam_idx: torch.Tensor):
+        for name in list(self.t):
+            if name not in ("blk", "pos"):
+                self.t[name] = self.t[name].index_select(0, beam_idx.to(self.dev))
+        self.B = self.t["kc"].shape[0]
+
+
+class AKVLayer:
+    """One layer of the drop-in cache (akv/drop_in.py:169-873) with the warm tier
+    kept packed on the device.
+
+    ``update`` follows akv/drop_in.py:591-787: new tokens join the hot tier with
+    their positions; the importance vector decays by 0.3 and appends ones
+    (:375-389); past the (adaptive) budget the lowest-importance unprotected
+    tokens are chosen on the device (``select_demote_indices``), gathered and
+    quantized as one demotion event (one ``akv_quant_pack`` launch: keys per
+    channel over the event's tokens, values per token over all channels,
+    outliers per event and batch element, the reference's AffineQuantizer), and
+    the event's codes and scale / zero rows are appended to the packed tier --
+    no float16 working copy is kept.  The returned view is chronological: one
+    ``akv_dequant_unpack`` launch writes every warm token at its position and the
+    hot tokens are scattered in beside it (float16, or float32 when the hot
+    tokens are float32 / bfloat16, as the reference's torch.cat promotes).  The
+    measured packed bytes count codes + scale + zero per event
+    (packed_layout.measure_packed_bytes).
+
+    Each batch element is its own quantizer call over (H, n, D) -- the
+    reference's call on ``k.squeeze(0)`` at batch 1.  Warm-to-hot promotion
+    (:415-589) and per-head bit widths are not built: ``enable_promotion`` must be
+    False and ``per_head_bits`` unset (or of another head count, where the
+    reference falls back to the global widths)."""
+
+    def __init__(self, warm_bits: int = 3, hot_budget: int = 128, group_size: int = 64, protect: bool = False,
+                 enable_promotion: bool = True, promotion_threshold: float = 0.05,
+                 enable_promotion_proxy: bool = True, proxy_decay: float = 0.7, adaptive_hot_frac: float = 0.0,
+                 warm_key_bits: Optional[int] = None, warm_value_bits: Optional[int] = None,
+                 outlier_fraction: float = 0.0, per_head_bits: Optional[list] = None):
+        self.warm_bits = warm_bits
+        self.hot_budget = hot_budget
+        self.group_size = group_size
+        self.protect = protect
+        self.enable_promotion = enable_promotion
+        self.promotion_threshold = promotion_threshold
+        self.enable_promotion_proxy = enable_promotion_proxy
+        self.proxy_decay = proxy_decay
+        self.adaptive_hot_frac = adaptive_hot_frac
+        self.warm_key_bits = warm_key_bits or warm_bits
+        self.warm_value_bits = warm_value_bits or warm_bits
+        self.outlier_fraction = outlier_fraction
+        self.per_head_bits = list(per_head_bits) if per_head_bits is not None else None
+        self._hot_keys: Optional[torch.Tensor] = None
+        self._hot_values: Optional[torch.Tensor] = None
+        self._hot_positions: Optional[torch.Tensor] = None   # (N_hot,) int64, host
+        self._warm: Optional[_EventTier] = None
+        self._warm_positions: Optional[torch.Tensor] = None  # (N_warm,) int64, host
+        self._warm_len = 0
+        self._total_len = 0
+        self._warm_bytes_packed = 0
+        self._importance: Optional[torch.Tensor] = None      # (N_hot,) float32, device
+        self._decay = 0.3
+        self._step = 0
+        self.keys = self.values = None
+
+    def get_seq_length(self) -> int:
+        return self._total_len
+
+    def _append_hot(self, k, v, pos):
+        if self._hot_keys is None:
+            self._hot_keys, self._hot_values, self._hot_positions = k, v, pos
+        else:
+            self._hot_keys = torch.cat([self._hot_keys, k], dim=2)
+            self._hot_values = torch.cat([self._hot_values, v], dim=2)
+            self._hot_positions = torch.cat([self._hot_positions, pos])
+
+    def _update_importance(self, n_new: int, hot_len: int, device):
+        """akv/drop_in.py:375-389 (recency decay, on the device)."""
+        if self._importance is None or self._importance.shape[0] != hot_len - n_new:
+            self._importance = torch.ones(hot_len, dtype=torch.float32, device=device)
+        else:
+            self._importance = torch.cat([self._importance * self._decay,
+                                          torch.ones(n_new, dtype=torch.float32, device=device)])
+
+    def _demote(self, n_demote: int, hot_len: int):
+        hk, hv = self._hot_keys, self._hot_values
+        dev = hk.device
+        B, H, _, D = hk.shape
+        idx = select_demote_indices(self._importance, n_demote, hot_len, self.hot_budget, device=dev)
+        idx_host = idx.cpu()
+        positions = self._hot_positions[idx_host]
+        w = quantize_kv(hk, hv, self.warm_key_bits, self.warm_value_bits, block_t=max(n_demote, 1), group_v=D,
+                        outlier_fraction=self.outlier_fraction, sel=idx.unsqueeze(0).expand(B, n_demote))
+        if self._warm is None:
+            self._warm = _EventTier(B, H, D, self.warm_key_bits, self.warm_value_bits, w.n_out, dev)
+        self._warm.append(w, positions.to(dev))
+        # measure_packed_bytes per batch element: packed codes + fp16 scale and zero, K and V
+        self._warm_bytes_packed += (w.k_codes.nbytes + w.k_scale.nbytes + w.k_zero.nbytes
+                                    + w.v_codes.nbytes + w.v_scale.nbytes + w.v_zero.nbytes)
+        self._warm_positions = positions if self._warm_positions is None else torch.cat([self._warm_positions,
+                                                                                         positions])
+        self._warm_len += n_demote
+        keep = torch.ones(hot_len, dtype=torch.bool)
+        keep[idx_host] = False
+        keep_dev = keep.to(dev)
+        self._hot_keys = hk[:, :, keep_dev]
+        self._hot_values = hv[:, :, keep_dev]
+        self._hot_positions = self._hot_positions[keep]
+        self._importance = self._importance[keep_dev]
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor,
+               cache_kwargs: Optional[dict] = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """Append new KV, demote past the budget, return the chronological view."""
+        nat.require_device(key_states, value_states)
+        B, H, N, D = key_states.shape
+        new_positions = torch.arange(self._total_len, self._total_len + N, dtype=torch.long)
+        if self.protect:
+            self._append_hot(key_states, value_states, new_positions)
+            self._total_len += N
+            self.keys, self.values = self._hot_keys, self._hot_values
+            return self._hot_keys, self._hot_values
+        if self.enable_promotion:
+            raise NotImplementedError("warm-to-hot promotion is not built for the packed warm tier; "
+                                      "construct the cache with enable_promotion=False")
+        if self.per_head_bits and len(self.per_head_bits) == H:
+            raise NotImplementedError("per-head bit widths are not built for the packed warm tier")
+        self._append_hot(key_states, value_states, new_positions)
+        self._total_len += N
+        self._step += 1
+        hot_len = self._hot_keys.shape[2]
+        self._update_importance(N, hot_len, key_states.device)
+        budget = self.hot_budget
+        if self.adaptive_hot_frac > 0.0:
+            budget = max(self.hot_budget, int(self.adaptive_hot_frac * self._total_len))
+        if hot_len > budget:
+            self._demote(hot_len - budget, hot_len)
+        if self._warm is None:
+            self.keys, self.values = self._hot_keys, self._hot_values
+            return self._hot_keys, self._hot_values
+        hk, hv = self._hot_keys, self._hot_values
+        out_dt = torch.float16 if hk.dtype == torch.float16 else torch.float32
+        fk = torch.empty(B, H, self._total_len, D, dtype=out_dt, device=hk.device)
+        fv = torch.empty_like(fk)
+        self._warm.dequantize_into(fk, fv)
+        hp = self._hot_positions.to(hk.device)
+        fk.index_copy_(2, hp, hk.to(out_dt))
+        fv.index_copy_(2, hp, hv.to(out_dt))
+        self.keys, self.values = fk, fv
+        return fk, fv
+
+    def warm_view(self) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
+        """The dequantized warm tier in demotion order (the reference's working copy)."""
+        if self._warm is None:
+            return None, None
+        w = self._warm
+        k = torch.empty(w.B, w.H, w.n, w.D, dtype=torch.float16, device=w.dev)
+        v = torch.empty_like(k)
+        w.dequantize_into(k, v, slots=False)
+        return k, v
+
+    def memory_usage_bytes(self) -> dict:
+        """akv/drop_in.py:789-873; ``warm_bytes_live`` is what the packed tier holds
+        resident (codes, meta, outlier values, event and position maps)."""
+        H, D = 1, 128
+        hot_bytes = 0
+        if self._hot_keys is not None:
+            hot_bytes = self._hot_keys.nbytes + self._hot_values.nbytes
+            H, D = self._hot_keys.shape[1], self._hot_keys.shape[3]
+        warm_live = self._warm.resident_bytes() if self._warm is not None else 0
+        packed = int(self._warm_bytes_packed)
+        formula = 0
+        if self._warm_len > 0:
+            groups = (D + self.group_size - 1) // self.group_size
+            formula = self._warm_len * ((H * D * self.warm_bits + 7) // 8 + groups * H * 4) * 2
+        total = hot_bytes + packed
+        fp16_equiv = self._total_len * H * D * 2 * 2
+        return {"hot_bytes": hot_bytes, "warm_bytes": packed, "warm_bytes_live": warm_live,
+                "warm_bytes_packed": packed, "warm_bytes_formula": formula, "total_bytes": total,
+                "fp16_equivalent_bytes": fp16_equiv, "savings_ratio": fp16_equiv / max(total, 1)}
+
+
 class AKVCache:
-    """Preset resolution and warm-tier settings of the drop-in cache
-    (akv/drop_in.py:885-964).  The HF ``DynamicCache`` wiring is not part of
-    this build; ``demote`` is the warm-tier hot path it drives."""
+    """The drop-in cache (akv/drop_in.py:885-1200): preset resolution, protected
+    layers, lazily created ``AKVLayer``s driven by ``update`` (the method an HF
+    model calls per layer), and ``demote`` (the warm-tier hot path with 32-token
+    K blocks, for callers that manage the tiers themselves).  Subclassing HF's
+    ``DynamicCache`` is not part of this build."""
 
     def __init__(self, preset: Optional[str] = None, warm_bits: Optional[int] = None,
                  warm_key_bits: Optional[int] = None, warm_value_bits: Optional[int] = None,
@@ -166,6 +466,106 @@ class AKVCache:
         self._protect_explicit = list(protect_layers) if protect_layers else []
         self.block_t = block_t
         self.group_v = group_v
+        # protected layers (akv/drop_in.py:971-998)
+        if protect_last > 0 and num_hidden_layers is None:
+            raise ValueError("protect_last requires num_hidden_layers. "
+                             "Use AKVCache.for_model(model, ...) or pass num_hidden_layers=.")
+        self._protected_set: set = set(range(protect_first))
+        if num_hidden_layers is not None:
+            for i in range(protect_last):
+                self._protected_set.add(num_hidden_layers - 1 - i)
+            for p in self._protect_explicit:
+                self._protected_set.add(p if p >= 0 else num_hidden_layers + p)
+        else:
+            for p in self._protect_explicit:
+                if p < 0:
+                    raise ValueError("Negative protect_layers indices require num_hidden_layers. "
+                                     "Use AKVCache.for_model(model, ...).")
+                self._protected_set.add(p)
+        self.layers: list = []
+        self._seen_tokens = 0
+        self._calibration_per_head_bits: dict = {}
+
+    def _is_protected(self, layer_idx: int) -> bool:
+        return layer_idx in self._protected_set
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,
+               cache_kwargs: Optional[dict] = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """akv/drop_in.py:1066-1096: create layers lazily, count tokens on layer 0, delegate."""
+        while len(self.layers) <= layer_idx:
+            idx = len(self.layers)
+            self.layers.append(AKVLayer(
+                warm_bits=self.warm_bits, hot_budget=self.hot_budget, group_size=self.group_size,
+                protect=self._is_protected(idx), enable_promotion=self.enable_promotion,
+                promotion_threshold=self.promotion_threshold, enable_promotion_proxy=self.enable_promotion_proxy,
+                proxy_decay=self.proxy_decay, adaptive_hot_frac=self.adaptive_hot_frac,
+                warm_key_bits=self.warm_key_bits, warm_value_bits=self.warm_value_bits,
+                outlier_fraction=self.outlier_fraction,
+                per_head_bits=self._calibration_per_head_bits.get(idx) if self._calibration_per_head_bits else None))
+        if layer_idx == 0:
+            self._seen_tokens += key_states.shape[2]
+        return self.layers[layer_idx].update(key_states, value_states, cache_kwargs)
+
+    def get_seq_length(self, layer_idx: int = 0) -> int:
+        return self.layers[layer_idx].get_seq_length() if layer_idx < len(self.layers) else 0
+
+    def get_usable_length(self, max_length: int, layer_idx: int = 0) -> int:
+        return self.get_seq_length(layer_idx)
+
+    def get_max_length(self) -> Optional[int]:
+        return None
+
+    @property
+    def seen_tokens(self) -> int:
+        return self._seen_tokens
+
+    @seen_tokens.setter
+    def seen_tokens(self, value: int):
+        self._seen_tokens = value
+
+    def reorder_cache(self, beam_idx: torch.Tensor):
+        """akv/drop_in.py:1119-1128: reorder the batch axis of both tiers."""
+        for layer in self.layers:
+            if layer._hot_keys is not None:
+                layer._hot_keys = layer._hot_keys.index_select(0, beam_idx)
+                layer._hot_values = layer._hot_values.index_select(0, beam_idx)
+            if layer._warm is not None:
+                layer._warm.index_batch(beam_idx)
+
+    def memory_usage(self) -> dict:
+        """akv/drop_in.py:1130-1160."""
+        keys = ("hot_bytes", "warm_bytes", "warm_bytes_live", "warm_bytes_packed", "warm_bytes_formula",
+                "total_bytes", "fp16_equivalent_bytes")
+        totals = {k: 0 for k in keys}
+        for layer in self.layers:
+            stats = layer.memory_usage_bytes()
+            for k in keys:
+                totals[k] += stats.get(k, 0)
+        totals["savings_ratio"] = totals["fp16_equivalent_bytes"] / max(totals["total_bytes"], 1)
+        totals["num_layers"] = len(self.layers)
+        return totals
+
+    def memory_report(self) -> dict:
+        """akv/drop_in.py:1162-1184."""
+        stats = self.memory_usage()
+        return {"compressed_bytes": stats["total_bytes"], "fp16_equiv_bytes": stats["fp16_equivalent_bytes"],
+                "savings_ratio": round(stats["savings_ratio"], 2), "key_bits": self.warm_key_bits,
+                "value_bits": self.warm_value_bits, "num_layers": stats["num_layers"],
+                "seq_length": self.get_seq_length(0)}
+
+    def __len__(self) -> int:
+        return len(self.layers)
+
+    def __getitem__(self, layer_idx: int):
+        """akv/drop_in.py:1188-1198: (warm working copy in demotion order, then hot)."""
+        if layer_idx < len(self.layers):
+            layer = self.layers[layer_idx]
+            if layer._hot_keys is not None:
+                wk, wv = layer.warm_view()
+                if wk is None:
+                    return layer._hot_keys, layer._hot_values
+                return (torch.cat([wk, layer._hot_keys], dim=2), torch.cat([wv, layer._hot_values], dim=2))
+        return torch.tensor([]), torch.tensor([])
 
     def demote(self, keys: torch.Tensor, values: torch.Tensor, importance: Optional[torch.Tensor],
                n_demote: int) -> tuple[WarmTier, torch.Tensor]:

@@ -540,18 +540,29 @@ int akv_dequant_unpack(const akv_dequant_args *a, void *stream) {
     p.ks = w.k_scale; p.kz = w.k_zero; p.vs = w.v_scale; p.vz = w.v_zero;
     p.out_dt = a->out_dtype;
     p.k_out = a->k_out; p.v_out = a->v_out;
+    const bool events = a->block_of_token != nullptr;
+    if (a->token_stride != 0 && a->token_stride < w.n_warm) return fail(AKV_E_SHAPE, "token_stride < n_warm");
+    if (a->out_slot && a->out_tokens < 1) return fail(AKV_E_SHAPE, "out_slot needs out_tokens >= 1");
+    p.tok_stride = a->token_stride > 0 ? a->token_stride : w.n_warm;
+    p.out_slot = a->out_slot;
+    p.out_tokens = a->out_tokens;
     if (w.kind == AKV_WARM_AFFINE) {
         for (int bits : {w.bits_k, w.bits_v})
             if ((bits < 2 || bits > 4) && bits != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
         if (w.block_t < 1 || w.group_v < 1 || a->D % w.group_v) return fail(AKV_E_SHAPE, "bad block_t / group_v");
-        if (a->out_dtype != AKV_DT_F16) return fail(AKV_E_DTYPE, "affine dequant produces float16");
+        if (a->out_dtype != AKV_DT_F16 && a->out_dtype != AKV_DT_F32)
+            return fail(AKV_E_DTYPE, "affine dequant produces float16 (or float32 holding float16 values)");
+        if (events && a->n_blocks < 1) return fail(AKV_E_SHAPE, "block_of_token needs n_blocks >= 1");
         p.nbh = a->B * a->Hkv; p.Hkv = a->Hkv;
         p.kc_row = a->D * w.bits_k / 8; p.vc_row = a->D * w.bits_v / 8;
         p.T = w.block_t; p.Gv = w.group_v;
-        p.nblk = (w.n_warm + w.block_t - 1) / w.block_t;
+        p.nblk = events ? a->n_blocks : (w.n_warm + w.block_t - 1) / w.block_t;
+        p.blk_of = a->block_of_token;
         p.n_out = w.n_out;
         p.k_oidx = w.k_oidx; p.v_oidx = w.v_oidx; p.k_odata = w.k_odata; p.v_odata = w.v_odata;
     } else if (w.kind == AKV_WARM_LEGACY) {
+        if (events || a->out_slot || (a->token_stride != 0 && a->token_stride != w.n_warm))
+            return fail(AKV_E_INVALID, "event blocks, token strides and output slots apply to the affine tier");
         if (w.bits_k != w.bits_v) return fail(AKV_E_BITS, "legacy warm tier uses one width for K and V");
         if (w.bits_k != 2 && w.bits_k != 4 && w.bits_k != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", w.bits_k);
         if (w.group_size < 1) return fail(AKV_E_SHAPE, "bad group_size");

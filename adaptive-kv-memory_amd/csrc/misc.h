@@ -23,6 +23,10 @@ struct DequantParams {
     const int *sym_flags;
     int out_dt;
     void *k_out, *v_out;
+    const int32_t *blk_of;        // affine: K-meta / outlier block of each token (else t / T)
+    int64_t tok_stride;           // token rows per (bh) of codes, V meta, outlier values
+    const int64_t *out_slot;      // output token row of each token (else the token's own row)
+    int64_t out_tokens;           // output token rows per (bh) when out_slot is set
 };
 
 struct ImportanceParams {

@@ -15,9 +15,11 @@ __global__ __launch_bounds__(256) void dequant_kernel(const DequantParams p) {
     const int64_t task = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t rows = (int64_t)p.nbh * p.n_warm;
     if (task >= rows * nch) return;
-    const int64_t row = task / nch;  // (bh, token)
     const int ch8 = (int)(task % nch);
-    const int64_t bh = row / p.n_warm, t = row % p.n_warm;
+    const int64_t bh = task / nch / p.n_warm, t = task / nch % p.n_warm;
+    const int64_t row = bh * p.tok_stride + t;  // input row (bh, token)
+    const int64_t blk = p.blk_of ? (int64_t)p.blk_of[t] : t / p.T;
+    const int64_t orow = p.out_slot ? bh * p.out_tokens + p.out_slot[t] : bh * p.n_warm + t;
     for (int which = 0; which < 2; ++which) {
         void *out = which == 0 ? p.k_out : p.v_out;
         if (!out) continue;
@@ -31,8 +33,8 @@ __global__ __launch_bounds__(256) void dequant_kernel(const DequantParams p) {
             const uint32_t c = extract_code(codes, d, bits);
             if (p.kind == AKV_WARM_AFFINE) {
                 int64_t mi;
-                if (which == 0) mi = (bh * p.nblk + t / p.T) * p.D + d;           // per channel, per block
-                else mi = (bh * p.n_warm + t) * (p.D / p.Gv) + d / p.Gv;          // per token, per group
+                if (which == 0) mi = (bh * p.nblk + blk) * p.D + d;              // per channel, per block
+                else mi = row * (p.D / p.Gv) + d / p.Gv;                          // per token, per group
                 const _Float16 s = ((const _Float16 *)sc)[mi], z = ((const _Float16 *)ze)[mi];
                 _Float16 v = (_Float16)c * s;
                 v = v + z;
@@ -51,7 +53,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const DequantParams p) {
             }
         }
         if (p.kind == AKV_WARM_AFFINE && p.n_out > 0) {
-            const int64_t *oi = (which == 0 ? p.k_oidx : p.v_oidx) + ((bh / p.Hkv) * p.nblk + t / p.T) * p.n_out;
+            const int64_t *oi = (which == 0 ? p.k_oidx : p.v_oidx) + ((bh / p.Hkv) * p.nblk + blk) * p.n_out;
             const _Float16 *od = (const _Float16 *)(which == 0 ? p.k_odata : p.v_odata) + row * p.n_out;
             for (int j = 0; j < p.n_out; ++j) {
                 const int d = (int)oi[j];
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const DequantParams p) {
                 }
             }
         }
-        const int64_t o = row * p.D + 8 * ch8;
+        const int64_t o = orow * p.D + 8 * ch8;
         for (int i = 0; i < 8; ++i) {
             if (p.out_dt == AKV_DT_F16) ((_Float16 *)out)[o + i] = (_Float16)vals[i];
             else if (p.out_dt == AKV_DT_BF16) ((uint16_t *)out)[o + i] = f32_to_bf16_rne(vals[i]);

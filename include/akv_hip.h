@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define AKV_ABI_VERSION 2
+#define AKV_ABI_VERSION 3
 
 /* status codes */
 #define AKV_OK 0
@@ -214,13 +214,27 @@ typedef struct akv_dequant_args {
     akv_warm_desc warm;
     void *k_out, *v_out;   /* [B][Hkv][Nw][D] (AFFINE) or [Hw][Nw][D] (LEGACY); either may be NULL */
     void *workspace;       /* >= 256 bytes of device scratch when warm.legacy_sym == -1, else unused */
+    /* AFFINE tiers built from blocks of any length (AKVLayer's demotion events, one
+     * block per event): all optional, 0 / NULL = the fixed block_t layout above. */
+    const int32_t *block_of_token; /* [Nw] K-meta / outlier block row of each warm token */
+    int64_t n_blocks;              /* K-meta rows per (batch, kv-head) and outlier-index rows per
+                                      batch element when block_of_token is given */
+    int64_t token_stride;          /* token rows per (batch, kv-head) of the codes, V meta and outlier
+                                      values (>= Nw; 0 = Nw) */
+    const int64_t *out_slot;       /* [Nw] output token row of each warm token: the outputs are then
+                                      [B][Hkv][out_tokens][D] and other rows are not written */
+    int64_t out_tokens;
 } akv_dequant_args;
 
 /* Unpack + dequantize a warm tier to dense values, bit-exact with
  * AffineQuantizer.dequantize_keys / dequantize_values
  * (akv/affine_quantizer.py:112-124, :178-189), triton_ops._dequantize_packed
  * (akv/triton_ops.py:657-713) and fused_attention._dequant_int4_tile
- * (akv/fused_attention.py:281-317). */
+ * (akv/fused_attention.py:281-317).  With block_of_token / out_slot it also
+ * serves AKVLayer's chronological view: the dequantized working copy of every
+ * demotion event (akv/drop_in.py:694-715) scattered to its tokens' positions
+ * (akv/drop_in.py:762-787).  AFFINE outputs are float16, or float32 holding the
+ * float16 values (the reference's cat with float32 / bfloat16 hot tokens). */
 int akv_dequant_unpack(const akv_dequant_args *args, void *stream);
 
 /* -------------------------------------------------------------- bitpack */

@@ -1,0 +1,136 @@
+"""AKVLayer / AKVCache.update with the packed warm tier against the oracle's
+restatement of the reference's update path (oracle/layer.py): every returned
+view bit-exact over prefill + decode + chunk sequences (fp16 views; float32
+views for bf16 / fp32 tokens), the measured packed bytes, the position
+bookkeeping, protected layers, __getitem__'s demotion-order view and
+reorder_cache."""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import announce
+from oracle.fp import BF16, F16, F32, to_dtype
+from oracle.layer import AKVLayerOracle
+
+pytestmark = pytest.mark.gpu
+
+_DT = {torch.float16: F16, torch.bfloat16: BF16, torch.float32: F32}
+
+
+def _tokens(rng, B, H, n, D, dtype):
+    x = (rng.standard_normal((B, H, n, D)) * 1.3).astype(np.float32)
+    x[..., 7] *= 8.0  # a loud channel (picked as the outlier when outliers are on)
+    host = to_dtype(x, _DT[dtype]).astype(np.float32)
+    t = torch.from_numpy(host).to(dtype).cuda()
+    return t, (host.astype(np.float16) if dtype == torch.float16 else host)
+
+
+def _same(got: torch.Tensor, want: np.ndarray, what: str):
+    g = got.cpu()
+    if g.dtype == torch.float16:
+        gv, wv = g.numpy().view(np.uint16), np.asarray(want, np.float16).view(np.uint16)
+    else:
+        gv, wv = g.float().numpy().view(np.uint32), np.asarray(want, np.float32).view(np.uint32)
+    assert gv.shape == wv.shape, f"{what}: shape {gv.shape} != {wv.shape}"
+    bad = np.count_nonzero(gv != wv)
+    assert bad == 0, f"{what}: {bad} of {gv.size} values differ"
+
+
+def _run(layer, orc, B, H, D, dtype, chunks, seed):
+    rng = np.random.default_rng(seed)
+    for step, n in enumerate(chunks):
+        announce(f"layer update step {step}: {n} tokens")
+        k, kh = _tokens(rng, B, H, n, D, dtype)
+        v, vh = _tokens(rng, B, H, n, D, dtype)
+        fk, fv = layer.update(k, v)
+        ok, ov, _ = orc.update(kh, vh, dt=_DT[dtype])
+        _same(fk, ok, f"K view after step {step}")
+        _same(fv, ov, f"V view after step {step}")
+        assert layer._total_len == orc.total_len and layer._warm_len == orc.warm_len
+        if orc.warm_pos is not None:
+            assert layer._warm_positions.tolist() == orc.warm_pos.tolist()
+        assert layer._hot_positions.tolist() == orc.hot_pos.tolist()
+        assert layer._warm_bytes_packed == orc.warm_bytes_packed
+
+
+@pytest.mark.parametrize("kb,vb,of,D", [(3, 3, 0.0, 128), (4, 2, 0.01, 128), (2, 2, 0.0, 64), (4, 4, 0.02, 128)])
+def test_update_views_match_oracle(kb, vb, of, D):
+    from akv.drop_in import AKVLayer
+    announce(f"AKVLayer K{kb}/V{vb} outliers {of} D={D}")
+    B, H = 2, 4
+    layer = AKVLayer(warm_bits=kb, warm_key_bits=kb, warm_value_bits=vb, hot_budget=64, outlier_fraction=of,
+                     enable_promotion=False)
+    orc = AKVLayerOracle(warm_bits=kb, warm_key_bits=kb, warm_value_bits=vb, hot_budget=64, outlier_fraction=of)
+    _run(layer, orc, B, H, D, torch.float16, [300] + [1] * 12 + [17, 1, 40], seed=kb * 10 + vb)
+    stats = layer.memory_usage_bytes()
+    assert 0 < stats["warm_bytes_packed"] < stats["fp16_equivalent_bytes"]
+    assert stats["warm_bytes_packed"] <= stats["warm_bytes_live"]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_update_non_fp16_tokens(dtype):
+    """bf16 / fp32 tokens: the demotion quantizes in that dtype, the view is float32
+    (float16 warm values beside the exact hot tokens, as torch.cat promotes)."""
+    from akv.drop_in import AKVLayer
+    announce(f"AKVLayer {dtype} tokens")
+    layer = AKVLayer(warm_bits=3, hot_budget=32, enable_promotion=False)
+    orc = AKVLayerOracle(warm_bits=3, hot_budget=32)
+    _run(layer, orc, 1, 2, 128, dtype, [100, 1, 1, 9], seed=4)
+
+
+def test_adaptive_budget_and_protected_layers():
+    from akv.drop_in import AKVCache
+    announce("AKVCache.update: protected first layer, adaptive budget")
+    B, H, D = 1, 2, 128
+    cache = AKVCache(warm_bits=4, hot_budget=32, adaptive_hot_frac=0.25, protect_first=1, enable_promotion=False,
+                     num_hidden_layers=3)
+    orcs = [None] + [AKVLayerOracle(warm_bits=4, hot_budget=32, adaptive_hot_frac=0.25) for _ in range(2)]
+    rng = np.random.default_rng(8)
+    seen = []
+    for step, n in enumerate([200, 1, 1, 30]):
+        k, kh = _tokens(rng, B, H, n, D, torch.float16)
+        v, vh = _tokens(rng, B, H, n, D, torch.float16)
+        seen.append(kh)
+        for li in range(3):
+            fk, fv = cache.update(k, v, li)
+            if li == 0:
+                _same(fk, np.concatenate(seen, axis=2), "protected layer")
+            else:
+                ok, ov, _ = orcs[li].update(kh, vh)
+                _same(fk, ok, f"layer {li} step {step}")
+                _same(fv, ov, f"layer {li} step {step}")
+    assert cache.seen_tokens == 232 and cache.get_seq_length(1) == 232
+    assert cache.layers[1]._hot_keys.shape[2] == max(32, int(0.25 * 232))
+    rep = cache.memory_report()
+    assert rep["num_layers"] == 3 and rep["seq_length"] == 232 and rep["savings_ratio"] > 1.0
+
+
+def test_getitem_and_reorder_cache():
+    from akv.drop_in import AKVCache
+    announce("AKVCache __getitem__ / reorder_cache")
+    B, H, D = 2, 2, 128
+    cache = AKVCache(warm_bits=3, hot_budget=16, enable_promotion=False)
+    orc = AKVLayerOracle(warm_bits=3, hot_budget=16)
+    rng = np.random.default_rng(5)
+    k, kh = _tokens(rng, B, H, 80, D, torch.float16)
+    v, vh = _tokens(rng, B, H, 80, D, torch.float16)
+    cache.update(k, v, 0)
+    orc.update(kh, vh)
+    gk, gv = cache[0]
+    _same(gk, np.concatenate([orc.warm_k, orc.hot_k], axis=2), "__getitem__ K (demotion order, then hot)")
+    _same(gv, np.concatenate([orc.warm_v, orc.hot_v], axis=2), "__getitem__ V")
+    cache.reorder_cache(torch.tensor([1, 0], device="cuda"))
+    k2, kh2 = _tokens(rng, B, H, 1, D, torch.float16)
+    fk, _ = cache.update(k2, k2, 0)
+    ok, _, _ = orc.update(kh2[::-1].copy(), kh2[::-1].copy())
+    _same(fk.flip(0), ok, "view after reorder_cache([1, 0])")
+
+
+def test_promotion_and_per_head_bits_are_refused():
+    from akv.drop_in import AKVLayer
+    announce("AKVLayer refuses promotion / per-head widths")
+    k = torch.zeros(1, 2, 4, 128, dtype=torch.float16, device="cuda")
+    with pytest.raises(NotImplementedError):
+        AKVLayer(hot_budget=2).update(k, k)
+    with pytest.raises(NotImplementedError):
+        AKVLayer(hot_budget=2, enable_promotion=False, per_head_bits=[2, 4]).update(k, k)
