@@ -239,6 +239,32 @@ class _EventTier:
         a.out_tokens = out_k.shape[2]
         nat.check(nat.load().akv_dequant_unpack(ctypes.byref(a), nat.stream_of(out_k)), "AKVLayer warm view")
 
+    def take(self, idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """The float16 values of warm tokens ``idx`` (warm-tier order), (B, H, n, D)."""
+        n = idx.numel()
+        sub = _EventTier.__new__(_EventTier)
+        sub.__dict__.update({k: v for k, v in self.__dict__.items() if k != "t"})
+        sub.t = {}
+        for name, x in self.t.items():
+            if name in self._TOKEN_AXIS:
+                sub.t[name] = x.narrow(self._TOKEN_AXIS[name], 0, self.n).index_select(self._TOKEN_AXIS[name], idx)
+            else:
+                sub.t[name] = x
+        sub.n, sub.cap = n, n
+        k = torch.empty(self.B, self.H, n, self.D, dtype=torch.float16, device=self.dev)
+        v = torch.empty_like(k)
+        sub.dequantize_into(k, v, slots=False)
+        return k, v
+
+    def keep(self, keep_mask: torch.Tensor):
+        """Drop the warm tokens where ``keep_mask`` is False (their events' K meta rows stay)."""
+        kept = keep_mask.nonzero().flatten()
+        for name, x in self.t.items():
+            if name in self._TOKEN_AXIS:
+                ax = self._TOKEN_AXIS[name]
+                x.narrow(ax, 0, kept.numel()).copy_(x.narrow(ax, 0, self.n).index_select(ax, kept))
+        self.n = kept.numel()
+
     def index_batch(self, beam_idx: torch.Tensor):
         for name in list(self.t):
             if name not in ("blk", "pos"):
@@ -265,10 +291,17 @@ class AKVLayer:
     measured packed bytes count codes + scale + zero per event
     (packed_layout.measure_packed_bytes).
 
+    Promotion (:415-589): with the proxy on, the EMA of |cos| between the mean
+    new key and each warm token's key (dequantized, averaged over batch and
+    heads) is kept per warm token; warm tokens above ``promotion_threshold`` --
+    by the attention weights' warm columns when ``cache_kwargs`` carries them,
+    else by the proxy -- return to the front of the hot tier with their float16
+    values and importance 2.0, at most max(1, hot_budget // 8) per step, and
+    leave the packed tier.
+
     Each batch element is its own quantizer call over (H, n, D) -- the
-    reference's call on ``k.squeeze(0)`` at batch 1.  Warm-to-hot promotion
-    (:415-589) and per-head bit widths are not built: ``enable_promotion`` must be
-    False and ``per_head_bits`` unset (or of another head count, where the
+    reference's call on ``k.squeeze(0)`` at batch 1.  Per-head bit widths are not
+    built: ``per_head_bits`` must be unset (or of another head count, where the
     reference falls back to the global widths)."""
 
     def __init__(self, warm_bits: int = 3, hot_budget: int = 128, group_size: int = 64, protect: bool = False,
@@ -298,6 +331,7 @@ class AKVLayer:
         self._total_len = 0
         self._warm_bytes_packed = 0
         self._importance: Optional[torch.Tensor] = None      # (N_hot,) float32, device
+        self._proxy_score: Optional[torch.Tensor] = None     # (N_warm,) float32, device
         self._decay = 0.3
         self._step = 0
         self.keys = self.values = None
@@ -321,6 +355,54 @@ class AKVLayer:
             self._importance = torch.cat([self._importance * self._decay,
                                           torch.ones(n_new, dtype=torch.float32, device=device)])
 
+    def _update_proxy_score(self, key_states: torch.Tensor):
+        """akv/drop_in.py:486-525 over the packed tier (its keys dequantized)."""
+        if self._warm is None or self._warm.n == 0:
+            self._proxy_score = None
+            return
+        probe = key_states.detach().float().mean(dim=(0, 1, 2))
+        probe = probe / (probe.norm() + 1e-6)
+        wk, _ = self._warm.take(torch.arange(self._warm.n, device=self._warm.dev))
+        wk_flat = wk.float().mean(dim=(0, 1))
+        wk_norm = wk_flat / (wk_flat.norm(dim=-1, keepdim=True) + 1e-6)
+        sim = wk_norm @ probe
+        if self._proxy_score is None or self._proxy_score.shape[0] != sim.shape[0]:
+            self._proxy_score = sim.abs()
+        else:
+            d = self.proxy_decay
+            self._proxy_score = d * self._proxy_score + (1 - d) * sim.abs()
+
+    def _promote(self, scores: torch.Tensor, use_proxy: bool):
+        """akv/drop_in.py:433-484 / :543-589: move the warm tokens above the threshold
+        (at most max(1, hot_budget // 8), the top ones) to the front of the hot tier."""
+        warm_len = self._warm.n
+        mask = scores > self.promotion_threshold
+        n = int(mask.sum().item())
+        if n == 0:
+            return
+        cap = max(1, self.hot_budget // 8)
+        if n > cap:
+            _, top = scores.topk(cap)
+            mask = torch.zeros_like(mask)
+            mask[top] = True
+            n = cap
+        idx = mask.nonzero().flatten()
+        pk, pv = self._warm.take(idx)
+        idx_host = idx.cpu()
+        positions = self._warm_positions[idx_host]
+        keep = ~mask
+        self._warm.keep(keep)
+        self._warm_positions = self._warm_positions[keep.cpu()]
+        if use_proxy:
+            self._proxy_score = self._proxy_score[keep]
+        self._warm_bytes_packed = int(self._warm_bytes_packed * (max(0, warm_len - n) / warm_len))
+        self._warm_len -= n
+        self._hot_keys = torch.cat([pk, self._hot_keys], dim=2)
+        self._hot_values = torch.cat([pv, self._hot_values], dim=2)
+        self._hot_positions = torch.cat([positions, self._hot_positions])
+        if self._importance is not None:
+            self._importance = torch.cat([torch.full((n,), 2.0, device=self._importance.device), self._importance])
+
     def _demote(self, n_demote: int, hot_len: int):
         hk, hv = self._hot_keys, self._hot_values
         dev = hk.device
@@ -339,6 +421,9 @@ class AKVLayer:
         self._warm_positions = positions if self._warm_positions is None else torch.cat([self._warm_positions,
                                                                                          positions])
         self._warm_len += n_demote
+        if self._proxy_score is not None:  # new warm tokens start with no evidence
+            self._proxy_score = torch.cat([self._proxy_score,
+                                           torch.zeros(n_demote, dtype=self._proxy_score.dtype, device=dev)])
         keep = torch.ones(hot_len, dtype=torch.bool)
         keep[idx_host] = False
         keep_dev = keep.to(dev)
@@ -358,9 +443,6 @@ class AKVLayer:
             self._total_len += N
             self.keys, self.values = self._hot_keys, self._hot_values
             return self._hot_keys, self._hot_values
-        if self.enable_promotion:
-            raise NotImplementedError("warm-to-hot promotion is not built for the packed warm tier; "
-                                      "construct the cache with enable_promotion=False")
         if self.per_head_bits and len(self.per_head_bits) == H:
             raise NotImplementedError("per-head bit widths are not built for the packed warm tier")
         self._append_hot(key_states, value_states, new_positions)
@@ -368,6 +450,18 @@ class AKVLayer:
         self._step += 1
         hot_len = self._hot_keys.shape[2]
         self._update_importance(N, hot_len, key_states.device)
+        if self.enable_promotion_proxy:
+            self._update_proxy_score(key_states)
+        if self.enable_promotion and cache_kwargs and "attention_weights" in cache_kwargs:
+            aw = cache_kwargs["attention_weights"]
+            if self._warm is not None and self._warm.n and aw.dim() == 4 and aw.shape[-1] >= self._warm.n + hot_len:
+                self._promote(aw[:, :, :, : self._warm.n].float().mean(dim=(0, 1, 2)), use_proxy=False)
+            hot_len = self._hot_keys.shape[2]
+        elif self.enable_promotion and self.enable_promotion_proxy:
+            if (self._proxy_score is not None and self._warm is not None and self._warm.n
+                    and self._proxy_score.shape[0] == self._warm.n):
+                self._promote(self._proxy_score, use_proxy=True)
+            hot_len = self._hot_keys.shape[2]
         budget = self.hot_budget
         if self.adaptive_hot_frac > 0.0:
             budget = max(self.hot_budget, int(self.adaptive_hot_frac * self._total_len))

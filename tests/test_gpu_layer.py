@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import announce
+from gpu_util import announce, to_dev
 from oracle.fp import BF16, F16, F32, to_dtype
 from oracle.layer import AKVLayerOracle
 
@@ -126,11 +126,65 @@ def test_getitem_and_reorder_cache():
     _same(fk.flip(0), ok, "view after reorder_cache([1, 0])")
 
 
-def test_promotion_and_per_head_bits_are_refused():
+def test_per_head_bits_are_refused():
     from akv.drop_in import AKVLayer
-    announce("AKVLayer refuses promotion / per-head widths")
+    announce("AKVLayer refuses per-head widths")
     k = torch.zeros(1, 2, 4, 128, dtype=torch.float16, device="cuda")
     with pytest.raises(NotImplementedError):
-        AKVLayer(hot_budget=2).update(k, k)
-    with pytest.raises(NotImplementedError):
         AKVLayer(hot_budget=2, enable_promotion=False, per_head_bits=[2, 4]).update(k, k)
+    # another head count: the reference falls back to the global widths
+    AKVLayer(hot_budget=2, enable_promotion=False, per_head_bits=[2, 4, 4]).update(k, k)
+
+
+def test_promotion_from_attention_weights():
+    """Warm columns of the attention weights above the threshold (6 of them, cap 4):
+    the top 4 return to the front of the hot tier with their float16 values."""
+    from akv.drop_in import AKVLayer
+    announce("AKVLayer promotion from attention weights")
+    B, H, D = 1, 2, 128
+    layer = AKVLayer(warm_bits=3, hot_budget=32, enable_promotion=True, enable_promotion_proxy=False)
+    orc = AKVLayerOracle(warm_bits=3, hot_budget=32, enable_promotion=True, enable_promotion_proxy=False)
+    rng = np.random.default_rng(11)
+    k, kh = _tokens(rng, B, H, 100, D, torch.float16)
+    v, vh = _tokens(rng, B, H, 100, D, torch.float16)
+    layer.update(k, v)
+    orc.update(kh, vh)
+    warm_len, hot_len = orc.warm_len, orc.hot_k.shape[2]
+    aw = np.full((B, H, 1, warm_len + hot_len + 1), 0.001, np.float32)
+    aw[..., [3, 10, 11, 20, 40, 50]] = [0.2, 0.5, 0.06, 0.3, 0.07, 0.4]
+    for step in range(3):
+        k, kh = _tokens(rng, B, H, 1, D, torch.float16)
+        v, vh = _tokens(rng, B, H, 1, D, torch.float16)
+        fk, fv = layer.update(k, v, {"attention_weights": to_dev(aw)} if step == 0 else None)
+        ok, ov, _ = orc.update(kh, vh, attention_weights=aw if step == 0 else None)
+        _same(fk, ok, f"K view after step {step}")
+        _same(fv, ov, f"V view after step {step}")
+        assert layer._hot_positions.tolist() == orc.hot_pos.tolist()
+        assert layer._warm_positions.tolist() == orc.warm_pos.tolist()
+        assert layer._warm_bytes_packed == orc.warm_bytes_packed
+        np.testing.assert_array_equal(layer._importance.cpu().numpy(), orc.importance)
+
+
+@pytest.mark.parametrize("threshold,decay", [(0.0, 0.0), (0.2, 0.7)])
+def test_proxy_promotion_matches_oracle(threshold, decay):
+    """The proxy (float32 reductions: within 2e-5 of the oracle's) and the
+    promotions it drives, over a prefill and decode steps; views bit-exact."""
+    from akv.drop_in import AKVLayer
+    announce(f"AKVLayer proxy promotion threshold={threshold} decay={decay}")
+    B, H, D = 2, 2, 128
+    layer = AKVLayer(warm_bits=4, hot_budget=24, enable_promotion=True, enable_promotion_proxy=True,
+                     promotion_threshold=threshold, proxy_decay=decay)
+    orc = AKVLayerOracle(warm_bits=4, hot_budget=24, enable_promotion=True, enable_promotion_proxy=True,
+                         promotion_threshold=threshold, proxy_decay=decay)
+    rng = np.random.default_rng(12)
+    for step, n in enumerate([120] + [1] * 10 + [5]):
+        k, kh = _tokens(rng, B, H, n, D, torch.float16)
+        v, vh = _tokens(rng, B, H, n, D, torch.float16)
+        fk, fv = layer.update(k, v)
+        ok, ov, _ = orc.update(kh, vh)
+        if orc.proxy is not None:
+            np.testing.assert_allclose(layer._proxy_score.cpu().numpy(), orc.proxy, rtol=2e-5, atol=2e-6)
+        _same(fk, ok, f"K view after step {step}")
+        _same(fv, ov, f"V view after step {step}")
+        assert layer._hot_positions.tolist() == orc.hot_pos.tolist()
+    assert orc.promoted_total > 0

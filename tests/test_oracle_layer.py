@@ -148,3 +148,114 @@ def test_event_working_copy_is_the_quantizer_round_trip():
     for b in range(2):
         qk = oaff.quantize_keys(k[b][:, pos], 2, 0.02)
         np.testing.assert_array_equal(layer.warm_k[b].view(np.uint16), oaff.dequantize_keys(qk).view(np.uint16))
+
+
+# ---------------------------------------------------------------- promotion
+
+def _step(layer, rng, H=4, D=8, n=1, direction=None, scale=1.0):
+    if direction is None:
+        k = (rng.standard_normal((1, H, n, D)) * scale).astype(np.float32)
+    else:
+        k = (np.broadcast_to(direction, (1, H, n, D)) + rng.standard_normal((1, H, n, D)) * 0.05).astype(np.float32)
+    v = (rng.standard_normal((1, H, n, D)) * scale).astype(np.float32)
+    return layer.update(k, v)
+
+
+def test_proxy_fires_without_attention_weights():
+    """tests/test_proxy_promotion.py:31-52 restated."""
+    layer = _layer(hot_budget=8, enable_promotion=True, enable_promotion_proxy=True, promotion_threshold=0.0,
+                   proxy_decay=0.0)
+    rng = np.random.default_rng(0)
+    for _ in range(16):
+        _step(layer, rng)
+    assert layer.warm_len > 0 and layer.proxy is not None and layer.proxy.shape[0] == layer.warm_len
+
+
+def test_proxy_disabled_skips_path():
+    layer = _layer(hot_budget=8, enable_promotion=True, enable_promotion_proxy=False)
+    rng = np.random.default_rng(1)
+    for _ in range(16):
+        _step(layer, rng)
+    assert layer.proxy is None
+
+
+def test_proxy_ranks_similar_warm_slot_highest():
+    """tests/test_proxy_promotion.py:72-133 restated."""
+    layer = _layer(warm_bits=4, hot_budget=16, enable_promotion=False, enable_promotion_proxy=True, proxy_decay=0.0)
+    rng = np.random.default_rng(7)
+    H, D = 4, 16
+    for _ in range(4):
+        _step(layer, rng, H, D)
+    target = rng.standard_normal(D).astype(np.float32)
+    target /= np.linalg.norm(target)
+    layer.update(np.broadcast_to(target, (1, H, 1, D)).astype(np.float32).copy(),
+                 rng.standard_normal((1, H, 1, D)).astype(np.float32))
+    for _ in range(40):
+        _step(layer, rng, H, D)
+    assert layer.warm_len > 0
+    layer.update((np.broadcast_to(target, (1, H, 1, D)) + 0.01 * rng.standard_normal((1, H, 1, D))).astype(np.float32),
+                 rng.standard_normal((1, H, 1, D)).astype(np.float32))
+    wk = layer.warm_k.astype(np.float32).mean(axis=(0, 1))
+    true = np.abs((wk / (np.linalg.norm(wk, axis=-1, keepdims=True) + 1e-6)) @ target)
+    assert int(np.argmax(layer.proxy)) == int(np.argmax(true))
+
+
+def test_proxy_score_resizes_on_demote():
+    layer = _layer(hot_budget=4, enable_promotion=True, enable_promotion_proxy=True, promotion_threshold=10.0,
+                   proxy_decay=0.5)
+    rng = np.random.default_rng(2)
+    for _ in range(8):
+        _step(layer, rng, 2, 8)
+    assert layer.warm_len > 0 and layer.proxy.shape[0] == layer.warm_len
+
+
+def test_proxy_closed_form():
+    """One proxy update against float64 evaluation of the same formula."""
+    layer = _layer(hot_budget=8, enable_promotion=False, enable_promotion_proxy=True, proxy_decay=0.7)
+    rng = np.random.default_rng(3)
+    for _ in range(12):
+        _step(layer, rng)
+    prev = layer.proxy.copy()
+    wk = layer.warm_k.astype(np.float64).mean(axis=(0, 1))
+    k = rng.standard_normal((1, 4, 1, 8)).astype(np.float32)
+    probe = k.astype(np.float64).mean(axis=(0, 1, 2))
+    probe /= np.linalg.norm(probe) + 1e-6
+    sim = np.abs((wk / (np.linalg.norm(wk, axis=-1, keepdims=True) + 1e-6)) @ probe)
+    layer.update(k, k)  # no demotion changes the warm set before the proxy update (8 hot + 1 -> 1 demoted after)
+    want = 0.7 * prev + 0.3 * sim
+    np.testing.assert_allclose(layer.proxy[: len(want)], want, rtol=2e-6, atol=1e-7)
+
+
+def test_promote_preserves_position_coverage():
+    """tests/test_cache_ordering.py:98-124 restated: threshold 0 promotes every step."""
+    N = 128
+    layer = _layer(hot_budget=16, enable_promotion=True, enable_promotion_proxy=True, promotion_threshold=0.0)
+    k, v = _pos_kv(N)
+    layer.update(k.astype(np.float32), v.astype(np.float32))
+    rng = np.random.default_rng(4)
+    for _ in range(8):
+        _step(layer, rng, 2, 8)
+    warm, hot = layer.warm_pos.tolist(), layer.hot_pos.tolist()
+    assert len(warm) + len(hot) == N + 8 and sorted(warm + hot) == list(range(N + 8))
+    assert layer.promoted_total >= 8  # max(1, 16 // 8) = 2 per step once the proxy is live
+
+
+def test_promotion_from_attention_weights():
+    """Warm columns above the threshold move to the front of the hot tier with
+    importance 2.0, at most max(1, budget // 8) of them (the top ones); the byte
+    counter keeps the kept fraction."""
+    layer = _layer(hot_budget=32, enable_promotion=True, enable_promotion_proxy=False, promotion_threshold=0.05)
+    k, v = _pos_kv(100)
+    layer.update(k, v)
+    warm_len, hot_len = layer.warm_len, layer.hot_k.shape[2]
+    aw = np.full((1, 2, 1, warm_len + hot_len + 1), 0.001, np.float32)
+    aw[..., [3, 10, 11, 20, 40, 50]] = [0.2, 0.5, 0.06, 0.3, 0.07, 0.4]  # 6 above the threshold, cap 4
+    bytes_before = layer.warm_bytes_packed
+    wpos = layer.warm_pos.copy()
+    z = np.zeros((1, 2, 1, 8), np.float16)
+    layer.update(z, z, attention_weights=aw)
+    top4 = sorted([10, 50, 20, 3])
+    assert layer.hot_pos[:4].tolist() == wpos[top4].tolist()
+    assert layer.warm_len == warm_len - 4 + 5  # 4 promoted, then 33 + 4 - 32 demoted back to the budget
+    assert set(wpos[top4].tolist()) <= set(layer.hot_pos.tolist())
+    assert layer.warm_bytes_packed >= int(bytes_before * (warm_len - 4) / warm_len)
