@@ -640,7 +640,11 @@ void decode_fast_kernel(const DecodeParams p) {
                         ov1[q] = *(const uint32_t *)(slot + L::VO + 2 * (16 * (q >> 1) + 4 * grp + 2 * (q & 1)));
                 }
             }
-            if (vfast) {
+            // One MFMA per channel chunk for both paths: the fast operand is always formed and a
+            // block whose -2^(10-o) s overflows (rare) overwrites it with the exact two-op form.
+            // A second MFMA on the accumulator in another branch would make the compiler keep
+            // the accumulators in two register sets and copy them every unit.
+            {
                 h2 vn[2][2][v_noffs<BV>()];
 #pragma unroll
                 for (int h = 0; h < 2; ++h)
@@ -660,23 +664,15 @@ void decode_fast_kernel(const DecodeParams p) {
                         const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
                         d[q] = as_u32(pk_fma(as_h2(uu), vs[h][pp], vn[h][pp][voff<BV>(kk) / v_ostep<BV>()]));
                     }
-                    if (OUT && kk == kk1) {
+                    if (__builtin_expect(!vfast, 0)) {
 #pragma unroll
-                        for (int q = 0; q < 4; ++q) d[q] = gsel1 ? ov1[q] : d[q];
-                    }
-                    stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
-                }
-            } else {
-#pragma unroll
-                for (int kk = 0; kk < 8; ++kk) {
-                    uint32_t d[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        const int h = q >> 1, pp = q & 1;
-                        const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
-                        const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
-                        const h2 c = as_h2(uu) - (h2){mv, mv};
-                        d[q] = as_u32(c * vs[h][pp]);
+                        for (int q = 0; q < 4; ++q) {
+                            const int h = q >> 1, pp = q & 1;
+                            const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
+                            const _Float16 mv = (_Float16)magic_val(voff<BV>(kk));
+                            const h2 c = as_h2(uu) - (h2){mv, mv};
+                            d[q] = as_u32(c * vs[h][pp]);
+                        }
                     }
                     if (OUT && kk == kk1) {
 #pragma unroll
