@@ -91,7 +91,11 @@ void make_plan(const akv_decode_args *a, Plan *pl) {
         // its waves share the range's hot tiles and warm units dynamically.
         const int64_t units = (nw + 31) / 32, tiles = (nh + 15) / 16;
         int64_t cp = a->num_splits > 0 ? a->num_splits : kCUs / pairs;
-        const int64_t by_items = (units + tiles) / (2 * akv::decode_fast_waves(w.n_out));
+        // Short contexts: about 3 items per 4 waves.  The launch then costs its fixed latency
+        // chain (first loads, one item, the merges) rather than several items per wave; more
+        // splits only lengthen the final merge (4k Qwen layer: 13.0 us at 2 items per wave,
+        // 10.3 us here, 11.3-12.2 us at 24-64 splits).
+        const int64_t by_items = (units + tiles) * 4 / (3 * akv::decode_fast_waves(w.n_out));
         if (a->num_splits <= 0 && cp > by_items) cp = by_items;
         if (cp < 1) cp = 1;
         pl->wsplit_len = (units + cp - 1) / cp * 32;
