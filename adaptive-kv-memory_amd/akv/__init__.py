@@ -9,6 +9,8 @@ from .bitpack import pack, unpack, packed_bytes
 from .drop_in import AKVCache, _PRESETS, select_demote_indices
 from .fused_attention import fused_int4_decode_attention, mixed_precision_decode_attention
 from .importance import ImportanceConfig, ImportanceScorer, ScoringStrategy
+from .packed_layout import PackedKVArena, PackedKVConfig, PagedKVCache
+from .production_cache import ProductionCache, ProductionCacheConfig
 from .quantizer import KVQuantizer, QuantConfig, QuantizedTensor
 from .triton_kernels import fused_decode_attention, fused_quantize_evict
 from .triton_ops import (
@@ -26,6 +28,7 @@ __all__ = [
     "AKVCache", "_PRESETS", "select_demote_indices",
     "fused_int4_decode_attention", "mixed_precision_decode_attention",
     "ImportanceConfig", "ImportanceScorer", "ScoringStrategy",
+    "PackedKVArena", "PackedKVConfig", "PagedKVCache", "ProductionCache", "ProductionCacheConfig",
     "KVQuantizer", "QuantConfig", "QuantizedTensor",
     "fused_decode_attention", "fused_quantize_evict",
     "HAS_TRITON", "fused_importance_update", "fused_mixed_precision_attention", "fused_quantized_attention",

@@ -13,7 +13,7 @@ from typing import Optional
 
 import torch
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 AKV_OK = 0
 AKV_E_INVALID = -1
@@ -53,6 +53,7 @@ class WarmDesc(ctypes.Structure):
         ("k_oidx", _vp), ("v_oidx", _vp),
         ("k_odata", _vp), ("v_odata", _vp),
         ("group_size", _i32), ("meta_dtype", _i32), ("warm_heads", _i32), ("legacy_sym", _i32),
+        ("token_stride", _i64),
     ]
 
 
@@ -68,6 +69,7 @@ class DecodeArgs(ctypes.Structure):
         ("n_scores", _i64),
         ("decay", ctypes.c_float), ("num_splits", _i32),
         ("workspace", _vp), ("workspace_bytes", _i64),
+        ("hot_stride", _i64),
     ]
 
 
@@ -104,7 +106,7 @@ class DequantArgs(ctypes.Structure):
         ("out_dtype", _i32), ("_pad0", _i32),
         ("warm", WarmDesc),
         ("k_out", _vp), ("v_out", _vp), ("workspace", _vp),
-        ("block_of_token", _vp), ("n_blocks", _i64), ("token_stride", _i64),
+        ("block_of_token", _vp), ("n_blocks", _i64),
         ("out_slot", _vp), ("out_tokens", _i64),
     ]
 

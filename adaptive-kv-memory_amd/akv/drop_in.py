@@ -216,6 +216,7 @@ class _EventTier:
         d.kind = nat.WARM_AFFINE
         d.bits_k, d.bits_v = self.bits_k, self.bits_v
         d.n_warm = self.n
+        d.token_stride = self.cap
         d.block_t = 1
         d.group_v = self.D
         d.n_out = self.n_out
@@ -233,7 +234,6 @@ class _EventTier:
         a.k_out, a.v_out = out_k.data_ptr(), out_v.data_ptr()
         a.block_of_token = t["blk"].data_ptr()
         a.n_blocks = self.ecap
-        a.token_stride = self.cap
         if slots:
             a.out_slot = t["pos"].data_ptr()
         a.out_tokens = out_k.shape[2]

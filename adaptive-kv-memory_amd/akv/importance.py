@@ -141,6 +141,40 @@ class ImportanceScorer:
     def get_scores(self, layer_idx: int) -> Optional[torch.Tensor]:
         return self._scores.get(layer_idx)
 
+    def get_eviction_candidates(self, layer_idx: int, seq_len: int, num_to_evict: int) -> torch.Tensor:
+        """akv/importance.py:245-300: ascending indices of the ``num_to_evict`` least
+        important of the first ``seq_len`` positions, the first
+        ``initial_tokens_protected`` and last ``recent_tokens_protected`` kept; FIFO takes
+        the oldest unprotected positions without scores.  Equal scores go lowest index
+        first (the reference's ``topk`` leaves their order open).  Empty (int64, on the
+        scores' device, or the host with none) when nothing is evictable."""
+        cfg = self.config
+        scores = self._scores.get(layer_idx)
+        dev = scores.device if scores is not None else torch.device("cpu")
+        empty = torch.empty(0, dtype=torch.long, device=dev)
+        if num_to_evict <= 0:
+            return empty
+        n_start = min(cfg.initial_tokens_protected, seq_len)
+        n_end = min(cfg.recent_tokens_protected, seq_len)
+        if cfg.strategy == ScoringStrategy.FIFO:
+            n = min(num_to_evict, max(0, seq_len - n_end - n_start))
+            return torch.arange(n_start, n_start + n, dtype=torch.long, device=dev) if n > 0 else empty
+        if scores is None:
+            return empty
+        s = scores[:seq_len].clone()
+        s[:n_start] = float("inf")
+        if n_end > 0:
+            s[-n_end:] = float("inf")
+        n = min(num_to_evict, int((s != float("inf")).sum().item()))
+        if n <= 0:
+            return empty
+        # the n smallest, ascending, equal scores lowest index first (one select launch)
+        src = nat.dev_contig(scores[:seq_len], torch.float32)
+        idx = torch.empty(n, dtype=torch.long, device=dev)
+        nat.check(nat.load().akv_select_demote(src.data_ptr(), 1, src.numel(), n, n_start, n_end, idx.data_ptr(),
+                                               nat.stream_of(src)), "get_eviction_candidates")
+        return idx
+
     def stats(self) -> dict:
         return {
             "num_layers_tracked": len(self._scores),

@@ -8,7 +8,8 @@ plus the ``group_mean`` / ``group_std`` / ``scale`` / ``zero`` tensors at their
 stored dtype.  Outlier channels are not counted (as in the reference).
 
 ``PackedKVArena`` is the reference's preallocated legacy-layout store
-(akv/packed_layout.py:56-281) with its quantize and dequantize on the device.
+(akv/packed_layout.py:56-281) with its quantize and dequantize on the device;
+``PagedKVCache`` its fp16 page pool (:283-443).
 """
 from __future__ import annotations
 
@@ -222,3 +223,90 @@ class PackedKVArena:
         self.valid[:remaining] = True
         self.valid[remaining:self._len] = False
         self._len = remaining
+
+
+class PagedKVCache:
+    """Fixed-size pages of fp16 K/V with per-layer page tables
+    (akv/packed_layout.py:283-443).  ``k_pool`` / ``v_pool`` are
+    (max_pages, heads, page_size, head_dim) device tensors; the page tables and free
+    list are host bookkeeping; appends are slice writes into the pool."""
+
+    def __init__(self, num_layers: int, num_heads: int, head_dim: int, page_size: int = 16, max_pages: int = 4096,
+                 dtype: torch.dtype = torch.float16, device: str = "cuda"):
+        if torch.device(device).type != "cuda":
+            raise RuntimeError("PagedKVCache lives on the GPU (device 'cuda')")
+        self.num_layers, self.num_heads, self.head_dim = num_layers, num_heads, head_dim
+        self.page_size, self.max_pages, self.dtype, self.device = page_size, max_pages, dtype, device
+        self.k_pool = torch.zeros(max_pages, num_heads, page_size, head_dim, dtype=dtype, device=device)
+        self.v_pool = torch.zeros(max_pages, num_heads, page_size, head_dim, dtype=dtype, device=device)
+        self._free_pages = list(range(max_pages))
+        self._used_pages: set = set()
+        self._page_tables: list[list[int]] = [[] for _ in range(num_layers)]
+        self._page_offsets: list[int] = [0] * num_layers
+        self._seq_lens: list[int] = [0] * num_layers
+
+    def allocate_page(self) -> int:
+        if not self._free_pages:
+            raise RuntimeError("Page pool exhausted")
+        page_id = self._free_pages.pop()
+        self._used_pages.add(page_id)
+        return page_id
+
+    def free_page(self, page_id: int):
+        if page_id in self._used_pages:
+            self._used_pages.discard(page_id)
+            self._free_pages.append(page_id)
+            self.k_pool[page_id].zero_()
+            self.v_pool[page_id].zero_()
+
+    def append(self, layer_idx: int, keys: torch.Tensor, values: torch.Tensor):
+        """keys / values (heads, N, head_dim): fill the layer's last page, then new ones."""
+        N = keys.shape[1]
+        offset = self._page_offsets[layer_idx]
+        table = self._page_tables[layer_idx]
+        pos = 0
+        while pos < N:
+            if offset == 0 or offset >= self.page_size:
+                table.append(self.allocate_page())
+                offset = 0
+            page_id = table[-1]
+            n = min(self.page_size - offset, N - pos)
+            self.k_pool[page_id, :, offset:offset + n] = keys[:, pos:pos + n]
+            self.v_pool[page_id, :, offset:offset + n] = values[:, pos:pos + n]
+            offset += n
+            pos += n
+        self._page_offsets[layer_idx] = offset
+        self._seq_lens[layer_idx] += N
+
+    def get_kv(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
+        """The layer's tokens gathered into (heads, seq_len, head_dim) tensors."""
+        seq_len = self._seq_lens[layer_idx]
+        if seq_len == 0:
+            e = torch.empty(self.num_heads, 0, self.head_dim, dtype=self.dtype, device=self.device)
+            return e, e.clone()
+        ids = torch.tensor(self._page_tables[layer_idx], dtype=torch.long, device=self.device)
+        k = self.k_pool[ids].permute(1, 0, 2, 3).reshape(self.num_heads, -1, self.head_dim)
+        v = self.v_pool[ids].permute(1, 0, 2, 3).reshape(self.num_heads, -1, self.head_dim)
+        return k[:, :seq_len], v[:, :seq_len]
+
+    def get_page_table(self, layer_idx: int) -> torch.Tensor:
+        return torch.tensor(self._page_tables[layer_idx], dtype=torch.int32, device=self.device)
+
+    def get_seq_length(self, layer_idx: int) -> int:
+        return self._seq_lens[layer_idx]
+
+    @property
+    def num_free_pages(self) -> int:
+        return len(self._free_pages)
+
+    @property
+    def memory_usage_mb(self) -> float:
+        return len(self._used_pages) * self.num_heads * self.page_size * self.head_dim * 2 * 2 / 1e6
+
+    def reset(self):
+        for table in self._page_tables:
+            for page_id in table:
+                self.free_page(page_id)
+            table.clear()
+        self._page_offsets = [0] * self.num_layers
+        self._seq_lens = [0] * self.num_layers

@@ -165,6 +165,11 @@ int check_decode(const akv_decode_args *a) {
         if (!aligned16(a->k_hot) || !aligned16(a->v_hot)) return fail(AKV_E_ALIGN, "hot tier must be 16-byte aligned");
         if (a->n_hot * a->D * 2 >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "hot tier per head exceeds 4 GiB");
     }
+    if (a->hot_stride != 0 && a->hot_stride < a->n_hot) return fail(AKV_E_SHAPE, "hot_stride < n_hot");
+    if (w.kind == AKV_WARM_AFFINE && w.token_stride != 0 && w.token_stride != w.n_warm)
+        return fail(AKV_E_UNSUPPORTED, "decode reads an affine warm tier with token_stride == n_warm only");
+    if (w.kind == AKV_WARM_LEGACY && w.token_stride != 0 && w.token_stride < w.n_warm)
+        return fail(AKV_E_SHAPE, "token_stride < n_warm");
     if (w.kind == AKV_WARM_AFFINE) {
         for (int bits : {w.bits_k, w.bits_v})
             if (bits < 2 || bits > 4) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
@@ -224,6 +229,8 @@ int check_prefill(const akv_prefill_args *a) {
         if (!aligned16(a->k_hot) || !aligned16(a->v_hot)) return fail(AKV_E_ALIGN, "hot tier must be 16-byte aligned");
         if (a->n_hot * a->D * 2 >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "hot tier per head exceeds 4 GiB");
     }
+    if (w.token_stride != 0 && w.token_stride != nw)
+        return fail(AKV_E_UNSUPPORTED, "prefill reads a warm tier with token_stride == n_warm only");
     if (w.kind == AKV_WARM_AFFINE) {
         for (int bits : {w.bits_k, w.bits_v})
             if (bits < 2 || bits > 4) return fail(AKV_E_BITS, "Unsupported bits: %d", bits);
@@ -315,8 +322,10 @@ int decode_run(const akv_decode_args *a, const Plan &pl, char *ctr, char *ws, vo
     p.q = (const _Float16 *)a->q;
     p.khot = (const _Float16 *)a->k_hot; p.vhot = (const _Float16 *)a->v_hot;
     p.n_hot = a->n_hot;
+    p.h_stride = a->hot_stride > 0 ? a->hot_stride : a->n_hot;
     const int wk = w.kind == AKV_WARM_NONE ? AKV_WARM_AFFINE : w.kind;
     p.n_warm = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
+    p.w_stride = w.token_stride > 0 ? w.token_stride : p.n_warm;
     int kb = 4, vb = 4;
     int sym_src[2] = {0, 0};
     const int *sym_ptr = nullptr;
@@ -545,9 +554,9 @@ int akv_dequant_unpack(const akv_dequant_args *a, void *stream) {
     p.out_dt = a->out_dtype;
     p.k_out = a->k_out; p.v_out = a->v_out;
     const bool events = a->block_of_token != nullptr;
-    if (a->token_stride != 0 && a->token_stride < w.n_warm) return fail(AKV_E_SHAPE, "token_stride < n_warm");
+    if (w.token_stride != 0 && w.token_stride < w.n_warm) return fail(AKV_E_SHAPE, "token_stride < n_warm");
     if (a->out_slot && a->out_tokens < 1) return fail(AKV_E_SHAPE, "out_slot needs out_tokens >= 1");
-    p.tok_stride = a->token_stride > 0 ? a->token_stride : w.n_warm;
+    p.tok_stride = w.token_stride > 0 ? w.token_stride : w.n_warm;
     p.out_slot = a->out_slot;
     p.out_tokens = a->out_tokens;
     if (w.kind == AKV_WARM_AFFINE) {
@@ -565,7 +574,7 @@ int akv_dequant_unpack(const akv_dequant_args *a, void *stream) {
         p.n_out = w.n_out;
         p.k_oidx = w.k_oidx; p.v_oidx = w.v_oidx; p.k_odata = w.k_odata; p.v_odata = w.v_odata;
     } else if (w.kind == AKV_WARM_LEGACY) {
-        if (events || a->out_slot || (a->token_stride != 0 && a->token_stride != w.n_warm))
+        if (events || a->out_slot || (w.token_stride != 0 && w.token_stride != w.n_warm))
             return fail(AKV_E_INVALID, "event blocks, token strides and output slots apply to the affine tier");
         if (w.bits_k != w.bits_v) return fail(AKV_E_BITS, "legacy warm tier uses one width for K and V");
         if (w.bits_k != 2 && w.bits_k != 4 && w.bits_k != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", w.bits_k);

@@ -13,10 +13,12 @@ struct DecodeParams {
     const _Float16 *q;
     const _Float16 *khot, *vhot;
     int64_t n_hot;
+    int64_t h_stride;             // hot token rows per (b, kv-head) (>= n_hot)
     // warm tier
     const void *kc, *vc;          // packed codes
     const void *ks, *kz, *vs, *vz; // meta
     int64_t n_warm;
+    int64_t w_stride;             // warm token rows per head (legacy; == n_warm for affine)
     int kc_row, vc_row;           // bytes per packed row
     int T, Gv;                    // affine: K token block, V channel group
     int tshift;                   // affine: log2(T / 32) when T / 32 is a power of two, else -1

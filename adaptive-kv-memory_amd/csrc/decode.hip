@@ -230,7 +230,7 @@ __device__ __forceinline__ void load_warm_tile(WarmRaw<D, KB, VB, WK> &R, const 
                 R.mz[i] = bld16(rvz, 2 * mi);
             } else {
                 const int tv = min(t0 + tt, nwarm - 1);
-                const int64_t gi = (hw * p.n_warm + tv) * ngr + gg;
+                const int64_t gi = (hw * p.w_stride + tv) * ngr + gg;
                 R.ms[i] = __builtin_bit_cast(uint32_t, load_as_f32(p.vs, gi, p.meta_dt));
                 R.mz[i] = __builtin_bit_cast(uint32_t, load_as_f32(p.vz, gi, p.meta_dt));
             }
@@ -238,7 +238,7 @@ __device__ __forceinline__ void load_warm_tile(WarmRaw<D, KB, VB, WK> &R, const 
     }
     if (WK == AKV_WARM_LEGACY) {  // K meta of this lane's token (groups covering its channels)
         const int ng = LCH / p.gs > 0 ? LCH / p.gs : 1;
-        const int64_t mrow = hw * p.n_warm + min(t0 + col, nwarm - 1);
+        const int64_t mrow = hw * p.w_stride + min(t0 + col, nwarm - 1);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             R.lks[q] = 0.f;
@@ -323,8 +323,8 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
 
     if (!is_warm) {
         // ------------------------------------------------------------ hot tiles
-        const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.khot + bh * p.n_hot * D, (uint32_t)(p.n_hot * D * 2));
-        const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vhot + bh * p.n_hot * D, (uint32_t)(p.n_hot * D * 2));
+        const __amdgpu_buffer_rsrc_t rk = make_rsrc(p.khot + bh * p.h_stride * D, (uint32_t)(p.n_hot * D * 2));
+        const __amdgpu_buffer_rsrc_t rv = make_rsrc(p.vhot + bh * p.h_stride * D, (uint32_t)(p.n_hot * D * 2));
         for (int t0 = t_begin + 16 * wave; t0 < t_end; t0 += 16 * kNW) {
             h8 kop[KSTEPS];
 #pragma unroll
@@ -362,14 +362,14 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
         const int64_t hw = (WK == AKV_WARM_AFFINE) ? bh : (p.warm_heads == 1 ? 0 : kvh);
         const int nwarm = (int)p.n_warm;
         const __amdgpu_buffer_rsrc_t rkc =
-            make_rsrc((const unsigned char *)p.kc + hw * p.n_warm * p.kc_row, (uint32_t)(p.n_warm * p.kc_row));
+            make_rsrc((const unsigned char *)p.kc + hw * p.w_stride * p.kc_row, (uint32_t)(p.n_warm * p.kc_row));
         const __amdgpu_buffer_rsrc_t rvc =
-            make_rsrc((const unsigned char *)p.vc + hw * p.n_warm * p.vc_row, (uint32_t)(p.n_warm * p.vc_row));
+            make_rsrc((const unsigned char *)p.vc + hw * p.w_stride * p.vc_row, (uint32_t)(p.n_warm * p.vc_row));
         const int ngr = (WK == AKV_WARM_AFFINE) ? D / p.Gv : p.lg;
         const __amdgpu_buffer_rsrc_t rvs =
-            make_rsrc((const _Float16 *)p.vs + hw * p.n_warm * ngr, (uint32_t)(p.n_warm * ngr * 2));
+            make_rsrc((const _Float16 *)p.vs + hw * p.w_stride * ngr, (uint32_t)(p.n_warm * ngr * 2));
         const __amdgpu_buffer_rsrc_t rvz =
-            make_rsrc((const _Float16 *)p.vz + hw * p.n_warm * ngr, (uint32_t)(p.n_warm * ngr * 2));
+            make_rsrc((const _Float16 *)p.vz + hw * p.w_stride * ngr, (uint32_t)(p.n_warm * ngr * 2));
         const __amdgpu_buffer_rsrc_t rks =
             make_rsrc((const _Float16 *)p.ks + bh * p.nblk * D, (uint32_t)(p.nblk * D * 2));
         const __amdgpu_buffer_rsrc_t rkz =

@@ -318,8 +318,8 @@ void decode_fast_kernel(const DecodeParams p) {
             R.vi = rsrc4(p.v_oidx + (int64_t)b * p.nblk * no, (uint32_t)(p.nblk * no * 8));
         }
     }
-    const u4 rkh = rsrc4(p.khot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
-    const u4 rvh = rsrc4(p.vhot + bh * p.n_hot * kD, (uint32_t)(p.n_hot * kD * 2));
+    const u4 rkh = rsrc4(p.khot + bh * p.h_stride * kD, (uint32_t)(p.n_hot * kD * 2));
+    const u4 rvh = rsrc4(p.vhot + bh * p.h_stride * kD, (uint32_t)(p.n_hot * kD * 2));
 
     // ---- the ring: a queue of NS slots, oldest first; a hot item is two units (K, then V)
     int qk[NS], qi[NS];

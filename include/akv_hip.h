@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define AKV_ABI_VERSION 3
+#define AKV_ABI_VERSION 4
 
 /* status codes */
 #define AKV_OK 0
@@ -85,6 +85,11 @@ typedef struct akv_warm_desc {
     int32_t meta_dtype;    /* AKV_DT_* of scales / zeros */
     int32_t warm_heads;    /* Hw: 1 or Hkv */
     int32_t legacy_sym;    /* -1 detect, 0 asymmetric, 1 symmetric */
+    /* token rows per warm head (LEGACY) or per (batch, kv-head) (AFFINE, dequant only) of
+     * the codes, V meta and outlier values, >= n_warm; 0 = n_warm.  Lets a preallocated
+     * store (PackedKVArena's [H][S][...] buffers, AKVLayer's growing tier) be read in
+     * place while only its first n_warm rows are filled. */
+    int64_t token_stride;
 } akv_warm_desc;
 
 /* ---------------------------------------------------------------- decode */
@@ -113,6 +118,8 @@ typedef struct akv_decode_args {
                               needs that region zeroed again, since the earlier call kept other data
                               there.  Calls that share a workspace must not overlap. */
     int64_t workspace_bytes;
+    int64_t hot_stride;    /* token rows per (batch, kv-head) of k_hot / v_hot, >= n_hot; 0 = n_hot
+                              (a preallocated hot buffer read in place) */
 } akv_decode_args;
 
 /* Bytes of device workspace akv_decode_attn needs for `args`. */
@@ -219,8 +226,6 @@ typedef struct akv_dequant_args {
     const int32_t *block_of_token; /* [Nw] K-meta / outlier block row of each warm token */
     int64_t n_blocks;              /* K-meta rows per (batch, kv-head) and outlier-index rows per
                                       batch element when block_of_token is given */
-    int64_t token_stride;          /* token rows per (batch, kv-head) of the codes, V meta and outlier
-                                      values (>= Nw; 0 = Nw) */
     const int64_t *out_slot;       /* [Nw] output token row of each warm token: the outputs are then
                                       [B][Hkv][out_tokens][D] and other rows are not written */
     int64_t out_tokens;

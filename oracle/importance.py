@@ -7,6 +7,10 @@
 (The Triton kernel at akv/triton_ops.py:288-323 divides by M; the torch path
 and ``ImportanceScorer`` sum over queries -- the sum is followed here.)
 
+``ImportanceScorer.get_eviction_candidates`` (akv/importance.py:245-300): the
+lowest scores of the first seq_len positions with the first / last protected
+windows kept, ascending; FIFO takes the oldest unprotected positions.
+
 ``ImportanceScorer.update`` (akv/importance.py:73-164): ATTENTION_ACCUMULATION
 and IMPORTANCE apply the same EMA on the first kv_len scores (growing the
 per-layer score vector with zeros); OBSERVATION_WINDOW sums only the last
@@ -23,7 +27,9 @@ Pinning: the decay KAT ``ones(32)``, zero attention, decay 0.5 -> 0.5
 (tests/test_triton_ops.py:169-174); float64 evaluation of the closed form;
 sum-over-queries vs mean checked at M > 1; the window and pooling against a
 direct float64 loop (tests/test_oracle_pinning.py); the policy strategies
-against their closed forms evaluated elementwise in float64.
+against their closed forms evaluated elementwise in float64; the eviction
+candidates against brute force over all subsets on tie-free inputs and the
+protected windows (tests/test_oracle_pinning.py).
 """
 from __future__ import annotations
 
@@ -88,3 +94,23 @@ def scorer_update(scores, attn, strategy="attention_accumulation", decay=0.95,
     else:
         raise ValueError(f"unknown strategy {strategy}")
     return scores
+
+
+def eviction_candidates(scores, seq_len: int, num_to_evict: int, strategy="importance", initial=4, recent=32):
+    """akv/importance.py:245-300 (ties: lowest index first, as oracle.selection)."""
+    if num_to_evict <= 0:
+        return np.zeros(0, np.int64)
+    n_start, n_end = min(initial, seq_len), min(recent, seq_len)
+    if strategy == "fifo":
+        n = min(num_to_evict, max(0, seq_len - n_end - n_start))
+        return np.arange(n_start, n_start + n, dtype=np.int64)
+    if scores is None:
+        return np.zeros(0, np.int64)
+    s = np.array(scores[:seq_len], dtype=np.float32, copy=True)
+    s[:n_start] = np.inf
+    if n_end > 0:
+        s[-n_end:] = np.inf
+    n = min(num_to_evict, int(np.sum(s != np.inf)))
+    if n <= 0:
+        return np.zeros(0, np.int64)
+    return np.sort(np.argsort(s, kind="stable")[:n]).astype(np.int64)

@@ -346,3 +346,24 @@ def test_observation_window_float64_loop():
             pad = ks // 2
             ki = [sum(ki[j] for j in range(n - pad, n - pad + ks) if 0 <= j < N) / ks for n in range(N)]
         np.testing.assert_allclose(got, ki, rtol=1e-5, atol=1e-7)
+
+
+def test_eviction_candidates_bruteforce():
+    """get_eviction_candidates (akv/importance.py:245-300): the unprotected subset of
+    the requested size with the smallest score sum, over every subset of tie-free
+    tiny inputs; FIFO takes the oldest unprotected; too few evictable -> fewer."""
+    import itertools
+    from oracle import importance as oimp
+    rng = np.random.default_rng(21)
+    for seq_len in (6, 9, 12):
+        for initial, recent in ((2, 1), (1, 3), (0, 0)):
+            s = rng.permutation(seq_len).astype(np.float32) + rng.random(seq_len).astype(np.float32) * 0.1
+            free = [i for i in range(seq_len) if i >= min(initial, seq_len) and i < seq_len - min(recent, seq_len)]
+            for k in range(0, len(free) + 2):
+                got = oimp.eviction_candidates(s, seq_len, k, "importance", initial, recent)
+                kk = min(k, len(free))
+                best = min(itertools.combinations(free, kk), key=lambda c: sum(float(s[i]) for i in c)) if kk else ()
+                assert got.tolist() == sorted(best)
+                fifo = oimp.eviction_candidates(None, seq_len, k, "fifo", initial, recent)
+                assert fifo.tolist() == free[:kk]
+    assert oimp.eviction_candidates(None, 10, 3, "importance").size == 0
