@@ -58,14 +58,21 @@ constexpr int kFusedMaxSplits = 32;
 
 bool fast_path(const akv_decode_args *a) {
     const akv_warm_desc &w = a->warm;
+    if (w.kind == AKV_WARM_LEGACY)  // per-token group meta, read like the affine V meta
+        return w.bits_k == w.bits_v && akv::decode_fast_legacy_shape(a->D, w.bits_k, w.group_size, w.meta_dtype) &&
+               akv::decode_fast_meta_aligned(w.token_stride > 0 ? w.token_stride : w.n_warm, w.group_size,
+                                             w.warm_heads) &&
+               akv::decode_fast_lds_bytes(akv::decode_fast_slot_bytes(w.bits_k, w.bits_v, w.group_size, 0, true), 0) <=
+                   160 * 1024;
     if (!(w.kind == AKV_WARM_AFFINE && a->D == 128 && w.block_t % 32 == 0 &&
-          (w.group_v == 32 || w.group_v == 64 || w.group_v == 128)))
+          (w.group_v == 32 || w.group_v == 64 || w.group_v == 128) &&
+          akv::decode_fast_meta_aligned(w.n_warm, w.group_v, (int64_t)a->B * a->Hkv)))
         return false;
     // outlier channels: up to 4 per block with 32-channel V groups; the ring must fit the LDS
     if (w.n_out != 0 && !(w.n_out <= 4 && w.group_v == 32 && w.k_odata && w.v_odata && w.k_oidx && w.v_oidx))
         return false;
-    return akv::decode_fast_lds_bytes(akv::decode_fast_slot_bytes(w.bits_k, w.bits_v, w.group_v, w.n_out), w.n_out) <=
-           160 * 1024;
+    return akv::decode_fast_lds_bytes(akv::decode_fast_slot_bytes(w.bits_k, w.bits_v, w.group_v, w.n_out, false),
+                                      w.n_out) <= 160 * 1024;
 }
 
 void make_plan(const akv_decode_args *a, Plan *pl) {
@@ -95,7 +102,8 @@ void make_plan(const akv_decode_args *a, Plan *pl) {
         // chain (first loads, one item, the merges) rather than several items per wave; more
         // splits only lengthen the final merge (4k Qwen layer: 13.0 us at 2 items per wave,
         // 10.3 us here, 11.3-12.2 us at 24-64 splits).
-        const int64_t by_items = (units + tiles) * 4 / (3 * akv::decode_fast_waves(w.n_out));
+        const int64_t by_items =
+            (units + tiles) * 4 / (3 * akv::decode_fast_waves(w.kind == AKV_WARM_AFFINE ? w.n_out : 0));
         if (a->num_splits <= 0 && cp > by_items) cp = by_items;
         if (cp < 1) cp = 1;
         pl->wsplit_len = (units + cp - 1) / cp * 32;
@@ -382,7 +390,11 @@ int decode_run(const akv_decode_args *a, const Plan &pl, char *ctr, char *ws, vo
     p.scores = a->scores;
     p.n_scores = a->scores ? a->n_scores : 0;
     p.decay = a->decay;
-    if (w.kind == AKV_WARM_AFFINE) p.slot_bytes = (int)akv::decode_fast_slot_bytes(kb, vb, w.group_v, w.n_out);
+    if (w.kind == AKV_WARM_AFFINE) p.slot_bytes = (int)akv::decode_fast_slot_bytes(kb, vb, w.group_v, w.n_out, false);
+    if (w.kind == AKV_WARM_LEGACY && fast_path(a)) {
+        p.Gv = w.group_size;
+        p.slot_bytes = (int)akv::decode_fast_slot_bytes(kb, vb, w.group_size, 0, true);
+    }
     hipError_t e = akv::decode_launch(p, kb, vb, wk, sym_ptr, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "decode launch");
     return ok();

@@ -66,9 +66,15 @@ hipError_t decode_reduce_launch(const DecodeParams &p, hipStream_t s);
 
 // LDS-streamed split kernel for the block-affine tier (decode_fast.hip).
 bool decode_fast_eligible(const DecodeParams &p, int wk);
-int64_t decode_fast_slot_bytes(int kb, int vb, int Gv, int n_out);
+int64_t decode_fast_slot_bytes(int kb, int vb, int Gv, int n_out, bool legacy);
+// The legacy (per-token group) layouts the fast kernel takes: head_dim 128, 2 or 4
+// bits, groups of 32 / 64 / 128 channels, fp16 scales and zeros.
+bool decode_fast_legacy_shape(int D, int bits, int group_size, int meta_dtype);
+// The fast kernel loads per-token meta rows of 1 or 2 groups in 16-byte pieces: with `heads`
+// tiers of `rows_per_head` token rows each, every tier's meta must start on 16 bytes.
+bool decode_fast_meta_aligned(int64_t rows_per_head, int Gv, int64_t heads);
 int64_t decode_fast_lds_bytes(int64_t slot_bytes, int n_out);
 int decode_fast_waves(int n_out);
-hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, hipStream_t s);
+hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, int wk, hipStream_t s);
 
 }  // namespace akv

@@ -1166,7 +1166,7 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
         if (e != hipSuccess) return e;
     }
     if (p.split_ctr && !decode_fast_eligible(p, wk)) return hipErrorInvalidValue;  // only the fast kernel merges
-    if (decode_fast_eligible(p, wk)) e = decode_fast_split_launch(p, kb, vb, s);
+    if (decode_fast_eligible(p, wk)) e = decode_fast_split_launch(p, kb, vb, wk, s);
     else e = (p.D == 64) ? launch_split_bits<64>(p, kb, vb, wk, s) : launch_split_bits<128>(p, kb, vb, wk, s);
     if (e != hipSuccess) return e;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M;

@@ -3,8 +3,14 @@
 //
 // Scope: head_dim 128, K blocks of T tokens with T a multiple of 32, V groups
 // of G = 32, 64 or 128 channels, 2/3/4 bits for K and V, and (variant OUT, V
-// groups of 32) up to 4 fp16 outlier channels per block.  Other shapes use
-// decode_split_kernel (decode.hip).
+// groups of 32) up to 4 fp16 outlier channels per block.  Variant LEG reads the
+// legacy per-token-group layout (the reference's public legacy ops and
+// PackedKVArena): 2 or 4 bits, one group size of 32 / 64 / 128 channels for K
+// and V, fp16 scales and zeros per (token, group), a warm tier per head or one
+// shared by all, rows w_stride apart; its K meta is loaded like V's, each lane's
+// 32 K channels share one (s, z), and K and V values are round16((c - offset) s
+// + z) in one fma (offset = half_max in the symmetric branch, else 0).  Other
+// shapes use decode_split_kernel (decode.hip).
 //
 // Work split: a 1-D grid over (split, kv-head, batch * row-chunk), renumbered
 // so that each XCD gets a contiguous run of items; a workgroup of 12 waves (8
@@ -93,18 +99,22 @@ constexpr int kAccRow = kD + 4;      // fp32 row of the end-of-split merge in LD
                                      // wave's 64 row/chunk writes over the banks)
 constexpr int kMaxOut = 4;            // outlier channels per block the fast kernel takes
 constexpr int kOutBytes = 2 * (kUnit * kMaxOut * 2) + 2 * 32;  // K/V outlier values + K/V indices
-template <int BK, int BV, int NG, bool OUT>
+template <int BK, int BV, int NG, bool OUT, bool LEG>
 struct WarmLayout {
     static constexpr int KR = 16 * BK, VR = 16 * BV;  // packed row bytes (D = 128)
     static constexpr int KCB = kUnit * KR, VCB = kUnit * VR;
     static constexpr int VMB = 64 * NG;               // V scale (or zero) bytes of 32 tokens
+    // K scale (or zero) bytes of a unit: the block's row of D channels, or (LEG) the 32
+    // tokens' rows of NG groups, laid out like V's
+    static constexpr int KMB = LEG ? VMB : 256;
     static constexpr int NKC = (KCB + 1023) / 1024, NVC = (VCB + 1023) / 1024;
     // full-lane load patterns (dma_lean) where the range sizes allow them
     static constexpr bool LEAN_C = dma_lean_ok<KCB>() && dma_lean_ok<VCB>();
     static constexpr bool LEAN_VM = dma_lean_ok<64 * NG>();
-    static constexpr int NLOAD = (LEAN_C ? dma_count<KCB>() + dma_count<VCB>() : NKC + NVC) + 2 +
+    static constexpr int NLOAD = (LEAN_C ? dma_count<KCB>() + dma_count<VCB>() : NKC + NVC) +
+                                 (LEG ? (LEAN_VM ? 2 * dma_count<64 * NG>() : 2) : 2) +
                                  (LEAN_VM ? 2 * dma_count<64 * NG>() : 2) + (OUT ? 4 : 0);
-    static constexpr int KC = 0, VC = KCB, KS = KCB + VCB, KZ = KS + 256, VS = KZ + 256, VZ = VS + VMB;
+    static constexpr int KC = 0, VC = KCB, KS = KCB + VCB, KZ = KS + KMB, VS = KZ + KMB, VZ = VS + VMB;
     // outlier channels: fp16 values [token][n_out] of K and V, int64 channel indices of the block
     static constexpr int KO = VZ + VMB, VO = KO + kUnit * kMaxOut * 2, KI = VO + kUnit * kMaxOut * 2, VI = KI + 32;
     static constexpr int BYTES = OUT ? VI + 32 : VZ + VMB;
@@ -115,10 +125,10 @@ struct WarmRes {
     u4 ko, vo, ki, vi;  // outlier values and indices
 };
 
-template <int BK, int BV, int NG, bool OUT>
+template <int BK, int BV, int NG, bool OUT, bool LEG>
 __device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T, int tshift,
                                            int n_out) {
-    using L = WarmLayout<BK, BV, NG, OUT>;
+    using L = WarmLayout<BK, BV, NG, OUT, LEG>;
     const uint32_t v16 = (uint32_t)lane * 16u, v4 = (uint32_t)lane * 4u;
     const uint32_t base = lds_addr(slot);
     if constexpr (L::LEAN_C) {
@@ -134,9 +144,19 @@ __device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot
     }
     // K block of the unit: T / 32 units per block (a shift when that is a power of two)
     const uint32_t blk = tshift >= 0 ? (uint32_t)u >> tshift : (uint32_t)((u * kUnit) / T);
-    const uint32_t kmrow = blk * 256u;
-    dma_lean<256>(R.ks, base + L::KS, kmrow, v16, v4);
-    dma_lean<256>(R.kz, base + L::KZ, kmrow, v16, v4);
+    if constexpr (LEG) {  // per-token rows of K meta, as V's
+        if constexpr (L::LEAN_VM) {
+            dma_lean<64 * NG>(R.ks, base + L::KS, (uint32_t)u * (uint32_t)L::VMB, v16, v4);
+            dma_lean<64 * NG>(R.kz, base + L::KZ, (uint32_t)u * (uint32_t)L::VMB, v16, v4);
+        } else {
+            dma16(R.ks, base + L::KS, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+            dma16(R.kz, base + L::KZ, v16, (uint32_t)u * (uint32_t)L::VMB, lane_mask(L::VMB));
+        }
+    } else {
+        const uint32_t kmrow = blk * 256u;
+        dma_lean<256>(R.ks, base + L::KS, kmrow, v16, v4);
+        dma_lean<256>(R.kz, base + L::KZ, kmrow, v16, v4);
+    }
     if constexpr (L::LEAN_VM) {
         dma_lean<64 * NG>(R.vs, base + L::VS, (uint32_t)u * (uint32_t)L::VMB, v16, v4);
         dma_lean<64 * NG>(R.vz, base + L::VZ, (uint32_t)u * (uint32_t)L::VMB, v16, v4);
@@ -233,13 +253,14 @@ __device__ __forceinline__ void wait_younger(int nw, int nh) {
     else wait_vm<0>();
 }
 
-template <int BK, int BV, int NG, int NS, bool OUT>
+template <int BK, int BV, int NG, int NS, bool OUT, bool LEG>
 __global__ __launch_bounds__(64 * FastCfg<OUT>::NW)
 __attribute__((amdgpu_waves_per_eu(FastCfg<OUT>::NW / 4, FastCfg<OUT>::NW / 4)))
 void decode_fast_kernel(const DecodeParams p) {
     constexpr int NW = FastCfg<OUT>::NW;  // waves of the workgroup
     static_assert(NS >= 2 && NS <= 4, "ring depth");
-    using L = WarmLayout<BK, BV, NG, OUT>;
+    static_assert(!(LEG && OUT), "the legacy layout has no outlier channels");
+    using L = WarmLayout<BK, BV, NG, OUT, LEG>;
     constexpr int KSTEPS = kD / 32;
     constexpr int NLW = L::NLOAD;     // loads of a warm unit
     constexpr int NLH = kHotLoads;    // loads of a hot half
@@ -279,6 +300,15 @@ void decode_fast_kernel(const DecodeParams p) {
     const int64_t strow = ((int64_t)(b * p.Hq + hq) * p.M + mq) * p.N;
     const int64_t bh = (int64_t)b * p.Hkv + kvh;
     const float sl2 = p.scale_log2;
+    // legacy layout: the symmetric branch ((code - half_max) s) per K / V, forced or detected
+    // by an earlier kernel on this stream
+    int symk = 0, symv = 0;
+    if constexpr (LEG) {
+        symk = __builtin_amdgcn_readfirstlane(p.sym_flags ? p.sym_flags[0] : p.legacy_sym);
+        symv = __builtin_amdgcn_readfirstlane(p.sym_flags ? p.sym_flags[1] : p.legacy_sym);
+    }
+    // code offsets of the legacy symmetric branch (0 otherwise)
+    const _Float16 hofk = (_Float16)(symk ? p.half_max_k : 0.f), hofv = (_Float16)(symv ? p.half_max_v : 0.f);
     const int64_t warm_base = p.hot_first ? p.n_hot : 0;  // logical position of warm token 0
     const int64_t hot_base = p.hot_first ? 0 : p.n_warm;
     // the stash rows are N floats apart: 16-byte stores need N and the segment base divisible by 4
@@ -304,12 +334,27 @@ void decode_fast_kernel(const DecodeParams p) {
     WarmRes R;
     {
         const uint32_t nwu = (uint32_t)p.n_warm;
-        R.kc = rsrc4((const unsigned char *)p.kc + bh * p.n_warm * L::KR, nwu * L::KR);
-        R.vc = rsrc4((const unsigned char *)p.vc + bh * p.n_warm * L::VR, nwu * L::VR);
-        R.ks = rsrc4((const _Float16 *)p.ks + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
-        R.kz = rsrc4((const _Float16 *)p.kz + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
-        R.vs = rsrc4((const _Float16 *)p.vs + bh * p.n_warm * NG, nwu * NG * 2);
-        R.vz = rsrc4((const _Float16 *)p.vz + bh * p.n_warm * NG, nwu * NG * 2);
+        // first token row of this (batch, kv-head)'s warm tier: dense per (batch, kv-head) for the
+        // block-affine layout; per warm head (shared by the batch, or by every head) and
+        // w_stride rows apart for the legacy layout
+        const int64_t wrow = LEG ? (int64_t)(p.warm_heads == 1 ? 0 : kvh) * p.w_stride : bh * p.n_warm;
+        R.kc = rsrc4((const unsigned char *)p.kc + wrow * L::KR, nwu * L::KR);
+        R.vc = rsrc4((const unsigned char *)p.vc + wrow * L::VR, nwu * L::VR);
+        // Per-token meta: with 4 groups a unit's rows are loaded a dword per lane, and every
+        // dword ends on a token; with 1 or 2 groups they come in 16-byte loads, and a load that
+        // crosses the end of the range may be dropped whole by the range check, so the range is
+        // rounded up to 16 bytes (the base is 16-byte aligned, so the last load lies in the
+        // page of its first byte) and the rows past the tier are cleared in LDS before use.
+        const uint32_t mrec = NG == 4 ? nwu * 8u : (nwu * NG * 2 + 15u) & ~15u;
+        if (LEG) {
+            R.ks = rsrc4((const _Float16 *)p.ks + wrow * NG, mrec);
+            R.kz = rsrc4((const _Float16 *)p.kz + wrow * NG, mrec);
+        } else {
+            R.ks = rsrc4((const _Float16 *)p.ks + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
+            R.kz = rsrc4((const _Float16 *)p.kz + bh * p.nblk * kD, (uint32_t)(p.nblk * kD * 2));
+        }
+        R.vs = rsrc4((const _Float16 *)p.vs + wrow * NG, mrec);
+        R.vz = rsrc4((const _Float16 *)p.vz + wrow * NG, mrec);
         if (OUT) {
             const int no = p.n_out;
             R.ko = rsrc4(p.k_odata + bh * p.n_warm * no, nwu * (uint32_t)no * 2);
@@ -351,7 +396,7 @@ void decode_fast_kernel(const DecodeParams p) {
         }
     };
     auto issue = [&](int k, int id, unsigned char *slot) {
-        if (k == kWarm) issue_warm<BK, BV, NG, OUT>(R, slot, lane, id, p.T, p.tshift, p.n_out);
+        if (k == kWarm) issue_warm<BK, BV, NG, OUT, LEG>(R, slot, lane, id, p.T, p.tshift, p.n_out);
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
@@ -454,29 +499,60 @@ void decode_fast_kernel(const DecodeParams p) {
         const int id = qi[0];
         unsigned char *slot = ring + head * slot_bytes;
         wait_head();
+        if (NG < 4 && id * kUnit + kUnit > nw) {
+            // the tail unit: meta rows past the tier's last token may hold bytes from outside it
+            const int t = lane & 31;
+            if (lane < 32 && t >= nw - id * kUnit) {
+#pragma unroll
+                for (int g = 0; g < NG; ++g) {
+                    *(_Float16 *)(slot + L::VS + 2 * (t * NG + g)) = (_Float16)0;
+                    *(_Float16 *)(slot + L::VZ + 2 * (t * NG + g)) = (_Float16)0;
+                    if (LEG) {
+                        *(_Float16 *)(slot + L::KS + 2 * (t * NG + g)) = (_Float16)0;
+                        *(_Float16 *)(slot + L::KZ + 2 * (t * NG + g)) = (_Float16)0;
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
         {
             // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS
             //      and read back per MFMA step; the fast paths hold when no -1024 s overflows
-            //      (K and V scales of the unit)
-            bool kfast, vfast;
-            {
+            //      (K and V scales of the unit).  LEG: the lane's 32 channels lie in one group,
+            //      so its token has one (s, z) per half, read from the slot; the value is
+            //      round16(c s + z) in one fma (the reference dequantizes this layout in fp32 and
+            //      rounds once), and the symmetric branch round16((c - half_max) s).
+            bool kfast = true, vfast;
+            h2 ls[2] = {}, lz[2] = {};
+            if constexpr (LEG) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int mo = 2 * ((16 * h + col) * NG + (32 * grp) / GV);
+                    const _Float16 sv = *(const _Float16 *)(slot + L::KS + mo);
+                    const _Float16 zv = symk ? (_Float16)0 : *(const _Float16 *)(slot + L::KZ + mo);
+                    ls[h] = (h2){sv, sv};
+                    lz[h] = (h2){zv, zv};
+                }
+            } else {
                 const h2 s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
                 const h2 z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
                 const h2 n2 = s2v * (h2){nmul, nmul};
                 const uint32_t nb = as_u32(n2);
                 kfast = !__builtin_amdgcn_ballot_w64(!finite2(nb));
-                bool vfin = true;
-                if (lane * 4 < L::VMB) {
-                    const h2 vsv = as_h2(*(const uint32_t *)(slot + L::VS + 4 * lane));
-                    const _Float16 n0 = (_Float16)(-1024.0f);
-                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
-                }
-                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
                 uint32_t *kmw = (uint32_t *)kmeta;
                 kmw[(0 * 4 + g2) * 16 + pi2] = as_u32(s2v);
                 kmw[(1 * 4 + g2) * 16 + pi2] = nb;
                 kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
                 __builtin_amdgcn_wave_barrier();
+            }
+            {
+                bool vfin = true;
+                if (!LEG && lane * 4 < L::VMB) {
+                    const h2 vsv = as_h2(*(const uint32_t *)(slot + L::VS + 4 * lane));
+                    const _Float16 n0 = (_Float16)(-1024.0f);
+                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
+                }
+                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
             }
             const u4 *kmr = (const u4 *)kmeta;
 
@@ -492,7 +568,26 @@ void decode_fast_kernel(const DecodeParams p) {
                 k_windows<BK>(kraw, W[h]);
             }
             f4 sc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-            if (kfast) {
+            if constexpr (LEG) {
+#pragma unroll
+                for (int st = 0; st < KSTEPS; ++st) {
+                    const h8 qst = qop(st);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        h8 a;
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) {
+                            const int pi = 4 * st + kk;
+                            const uint32_t uu = (k_window_of<BK>(W[h], pi) & km.m[koff<BK>(pi)]) | magic2(koff<BK>(pi));
+                            const _Float16 mv = (_Float16)magic_val(koff<BK>(pi)) + hofk;
+                            const h2 v = pk_fma(as_h2(uu) - (h2){mv, mv}, ls[h], lz[h]);  // (code - offset) s + z
+                            a[2 * kk] = v[0];
+                            a[2 * kk + 1] = v[1];
+                        }
+                        sc[h] = mfma_k32(a, qst, sc[h]);
+                    }
+                }
+            } else if (kfast) {
 #pragma unroll
                 for (int st = 0; st < KSTEPS; ++st) {
                     const u4 av = kmr[(0 * 4 + grp) * 4 + st], nv = kmr[(1 * 4 + grp) * 4 + st];
@@ -536,7 +631,6 @@ void decode_fast_kernel(const DecodeParams p) {
                     }
                 }
             }
-
             // ---- outlier channels of K: the stored fp16 value replaces the dequantized one,
             //      so q[c] * (value - dequant) joins the dot product.  A channel the
             //      quantizer zeroed has scale = zero = 0 and dequantizes to 0, which skips
@@ -618,6 +712,7 @@ void decode_fast_kernel(const DecodeParams p) {
                     const int ta = 16 * h + 2 * pp;  // + 4 grp (in vm_lane)
                     vs[h][pp] = lds_h2(slot + L::VS + vm_lane + ta * NG * 2, slot + L::VS + vm_lane + (ta + 1) * NG * 2);
                     vz[h][pp] = lds_h2(slot + L::VZ + vm_lane + ta * NG * 2, slot + L::VZ + vm_lane + (ta + 1) * NG * 2);
+                    if (LEG && symv) vz[h][pp] = (h2){(_Float16)0, (_Float16)0};  // symmetric: no zero-point
                 }
             uint32_t win[2][2][VSlot<BV>::NW];
 #pragma unroll
@@ -662,9 +757,14 @@ void decode_fast_kernel(const DecodeParams p) {
                     for (int q = 0; q < 4; ++q) {
                         const int h = q >> 1, pp = q & 1;
                         const uint32_t uu = (win[h][pp][vwin<BV>(kk)] & vmk.m[voff<BV>(kk)]) | magic2(voff<BV>(kk));
-                        d[q] = as_u32(pk_fma(as_h2(uu), vs[h][pp], vn[h][pp][voff<BV>(kk) / v_ostep<BV>()]));
+                        if constexpr (LEG) {  // round16((code - offset) s + z), z of the token pair
+                            const _Float16 mv = (_Float16)magic_val(voff<BV>(kk)) + hofv;
+                            d[q] = as_u32(pk_fma(as_h2(uu) - (h2){mv, mv}, vs[h][pp], vz[h][pp]));
+                        } else {
+                            d[q] = as_u32(pk_fma(as_h2(uu), vs[h][pp], vn[h][pp][voff<BV>(kk) / v_ostep<BV>()]));
+                        }
                     }
-                    if (__builtin_expect(!vfast, 0)) {
+                    if (!LEG && __builtin_expect(!vfast, 0)) {
 #pragma unroll
                         for (int q = 0; q < 4; ++q) {
                             const int h = q >> 1, pp = q & 1;
@@ -681,7 +781,7 @@ void decode_fast_kernel(const DecodeParams p) {
                     stt.acc[kk] = mfma_k32(__builtin_bit_cast(h8, (u4){d[0], d[1], d[2], d[3]}), pop, stt.acc[kk]);
                 }
             }
-            {
+            if constexpr (!LEG) {  // the zero-points of the block-affine V: sum_t P z per group
                 const h8 az8 = __builtin_bit_cast(h8, (u4){as_u32(vz[0][0]), as_u32(vz[0][1]), as_u32(vz[1][0]), as_u32(vz[1][1])});
                 stt.accz = mfma_k32(az8, pop, stt.accz);
             }
@@ -911,9 +1011,12 @@ void decode_fast_kernel(const DecodeParams p) {
 }
 
 // LDS slot of the fast kernel: one warm unit, or one 16-token hot K or V half.
-int64_t decode_fast_slot_bytes(int kb, int vb, int Gv, int n_out) {
+// K meta of a unit: two 256-byte block rows (block-affine) or two 64 NG-byte token
+// rows of groups (legacy).
+int64_t decode_fast_slot_bytes(int kb, int vb, int Gv, int n_out, bool legacy) {
     const int NG = kD / Gv;
-    int64_t warm = (int64_t)kUnit * 16 * (kb + vb) + 512 + 128 * NG + (n_out > 0 ? kOutBytes : 0);
+    int64_t warm = (int64_t)kUnit * 16 * (kb + vb) + (legacy ? 128 * NG : 512) + 128 * NG +
+                   (n_out > 0 ? kOutBytes : 0);
     int64_t s = warm > 4096 ? warm : 4096;
     return (s + 255) / 256 * 256;
 }
@@ -933,8 +1036,25 @@ int64_t decode_fast_lds_bytes(int64_t slot, int n_out) {
 }
 int decode_fast_waves(int n_out) { return n_out > 0 ? kWavesOut : kWaves; }
 
+bool decode_fast_legacy_shape(int D, int bits, int group_size, int meta_dtype) {
+    return D == kD && (bits == 2 || bits == 4) && (group_size == 32 || group_size == 64 || group_size == 128) &&
+           meta_dtype == AKV_DT_F16;
+}
+
+bool decode_fast_meta_aligned(int64_t rows_per_head, int Gv, int64_t heads) {
+    const int ng = kD / Gv;
+    return ng == 4 || heads <= 1 || (rows_per_head * ng * 2) % 16 == 0;
+}
+
 bool decode_fast_eligible(const DecodeParams &p, int wk) {
-    if (!(wk == AKV_WARM_AFFINE && p.D == kD && p.T % kUnit == 0 && (p.Gv == 32 || p.Gv == 64 || p.Gv == 128)))
+    if (wk == AKV_WARM_LEGACY) {
+        if (!(decode_fast_legacy_shape(p.D, p.kc_row * 8 / kD, p.gs, p.meta_dt) && p.kc_row == p.vc_row &&
+              p.Gv == p.gs && decode_fast_meta_aligned(p.w_stride, p.gs, p.warm_heads)))
+            return false;
+        return p.slot_bytes > 0 && decode_fast_lds_bytes(p.slot_bytes, 0) <= kLdsCap;
+    }
+    if (!(wk == AKV_WARM_AFFINE && p.D == kD && p.T % kUnit == 0 && (p.Gv == 32 || p.Gv == 64 || p.Gv == 128) &&
+          decode_fast_meta_aligned(p.n_warm, p.Gv, (int64_t)p.B * p.Hkv)))
         return false;
     // outlier channels: up to kMaxOut per block, V groups of 32 channels; the ring must fit the LDS
     if (p.n_out != 0 && !(p.n_out <= kMaxOut && p.Gv == 32 && p.k_odata && p.v_odata && p.k_oidx && p.v_oidx))
@@ -942,38 +1062,44 @@ bool decode_fast_eligible(const DecodeParams &p, int wk) {
     return p.slot_bytes > 0 && decode_fast_lds_bytes(p.slot_bytes, p.n_out) <= kLdsCap;
 }
 
-template <int BK, int BV, int NG, int NS, bool OUT>
+template <int BK, int BV, int NG, int NS, bool OUT, bool LEG>
 static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
     const dim3 grid((unsigned)(p.nsplit * p.Hkv * p.B * p.nchunk));  // decoded in the kernel
     const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes, OUT ? p.n_out : 0);
     static bool attr_set = false;  // raise the dynamic LDS cap above 64 KiB once
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS, OUT>,
+        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS, OUT, LEG>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCap);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
-    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG, NS, OUT>), grid, dim3(64 * FastCfg<OUT>::NW), lds, s, p);
+    hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG, NS, OUT, LEG>), grid, dim3(64 * FastCfg<OUT>::NW), lds, s, p);
     return hipGetLastError();
 }
 
-template <int BK, int BV, int NG>
+template <int BK, int BV, int NG, bool LEG>
 static hipError_t launch_fast(const DecodeParams &p, hipStream_t s) {
-    return launch_fast_ns<BK, BV, NG, kNS, false>(p, s);
+    return launch_fast_ns<BK, BV, NG, kNS, false, LEG>(p, s);
 }
 
-template <int BK, int BV>
+template <int BK, int BV, bool LEG>
 static hipError_t launch_fast_ng(const DecodeParams &p, hipStream_t s) {
-    if (p.n_out > 0) return p.Gv == 32 ? launch_fast_ns<BK, BV, 4, kNSOut, true>(p, s) : hipErrorInvalidValue;
-    if (p.Gv == 32) return launch_fast<BK, BV, 4>(p, s);
-    if (p.Gv == 64) return launch_fast<BK, BV, 2>(p, s);
-    if (p.Gv == 128) return launch_fast<BK, BV, 1>(p, s);
+    if (!LEG && p.n_out > 0)
+        return p.Gv == 32 ? launch_fast_ns<BK, BV, 4, kNSOut, true, false>(p, s) : hipErrorInvalidValue;
+    if (p.Gv == 32) return launch_fast<BK, BV, 4, LEG>(p, s);
+    if (p.Gv == 64) return launch_fast<BK, BV, 2, LEG>(p, s);
+    if (p.Gv == 128) return launch_fast<BK, BV, 1, LEG>(p, s);
     return hipErrorInvalidValue;
 }
 
-hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, hipStream_t s) {
+hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, int wk, hipStream_t s) {
+    if (wk == AKV_WARM_LEGACY) {
+        if (kb == 2 && vb == 2) return launch_fast_ng<2, 2, true>(p, s);
+        if (kb == 4 && vb == 4) return launch_fast_ng<4, 4, true>(p, s);
+        return hipErrorInvalidValue;
+    }
 #define AKV_FKV(a, b) \
-    if (kb == a && vb == b) return launch_fast_ng<a, b>(p, s);
+    if (kb == a && vb == b) return launch_fast_ng<a, b, false>(p, s);
     AKV_FKV(2, 2) AKV_FKV(2, 3) AKV_FKV(2, 4) AKV_FKV(3, 2) AKV_FKV(3, 3) AKV_FKV(3, 4) AKV_FKV(4, 2) AKV_FKV(4, 3)
     AKV_FKV(4, 4)
 #undef AKV_FKV

@@ -19,9 +19,11 @@ The line's "workloads" field summarises the other configurations, each
 measured after the headline on its own inputs (metric, value, roofline, CPU
 baseline): qwen_decode_4k (one Qwen layer at 4k context, 4/4-bit, with the
 reference CPU path beside it), llama7b_decode_16k (MHA, K4/V2 with outlier
-channels), llama3_demote_64k (select + gather + quantize + pack, 3-bit) and
-llama70b_prefill_128k (MFMA chunked prefill).  --workload NAME prints one of
-them on its own line instead.
+channels), llama3_demote_64k (select + gather + quantize + pack, 3-bit),
+llama70b_prefill_128k (MFMA chunked prefill) and production_decode_4k
+(ProductionCache.fused_attention over the 4-bit arenas at the cache's default
+sizes, with the reference's torch design timed beside it).  --workload NAME
+prints one of them on its own line instead.
 
 The roofline is taken on the attention-only replay (per layer: one launch of
 decode_fast_kernel, which also merges its splits): achieved = the op's
@@ -114,7 +116,7 @@ def main():
                     help="end with one device copy of 256 MiB (reference dispatch for counter runs)")
     ap.add_argument("--workload", default="qwen_decode_32k",
                     choices=["qwen_decode_32k", "llama7b_decode_16k", "llama70b_prefill_128k", "llama3_demote_64k",
-                             "qwen_decode_4k"],
+                             "qwen_decode_4k", "production_decode_4k"],
                     help="the headline decode step (default; the other workloads are summarised in its "
                          "'workloads' field), or one other workload on its own line")
     ap.add_argument("--no-other-workloads", action="store_true",
@@ -139,7 +141,8 @@ def main():
     from akv.warm_tier import DecodeCall
     if args.workload != "qwen_decode_32k":
         fn = {"llama70b_prefill_128k": bench_prefill, "llama3_demote_64k": bench_demote,
-              "llama7b_decode_16k": bench_decode_mha, "qwen_decode_4k": bench_c1}[args.workload]
+              "llama7b_decode_16k": bench_decode_mha, "qwen_decode_4k": bench_c1,
+              "production_decode_4k": bench_production}[args.workload]
         print(json.dumps(fn(args)), flush=True)
         return
 
@@ -248,7 +251,8 @@ def other_workloads(args):
     import torch
     out = {}
     for name, fn in (("qwen_decode_4k", bench_c1), ("llama7b_decode_16k", bench_decode_mha),
-                     ("llama3_demote_64k", bench_demote), ("llama70b_prefill_128k", bench_prefill)):
+                     ("llama3_demote_64k", bench_demote), ("llama70b_prefill_128k", bench_prefill),
+                     ("production_decode_4k", bench_production)):
         print(f"[bench] workload {name}", file=sys.stderr, flush=True)
         try:
             r = fn(args)
@@ -319,6 +323,112 @@ def bench_c1(args):
                                "sample": f"the whole layer (dequant + fp32 attention), {reps} runs, "
                                          f"{t_cpu:.1f} s on {cores} host threads",
                                "kv_gbps": round(nb["kv"] / (us * 1e-6) / 1e9, 4)}
+    return res
+
+
+def bench_production(args):
+    """ProductionCache.fused_attention at the reference's ProductionCacheConfig defaults
+    (akv/production_cache.py:33-70: 32 layers, 32 heads, head_dim 128, hot 1024 + warm
+    4096 tokens, group 64) with the minmax arenas at 4 bits: every layer's arenas full and
+    1024 hot tokens, one query token.  The 32 layers' calls (one decode launch each over
+    the packed arenas and the hot buffer) are captured in one graph; the working set
+    (1.14 GB) is beyond the 256 MB Infinity Cache.  Beside it, the reference's design on
+    the same GPU: the cached fp16 warm copy plus the hot tokens copied into one buffer,
+    then matmul / softmax / matmul (akv/production_cache.py:429-469)."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from akv.production_cache import ProductionCache, ProductionCacheConfig
+    from oracle import legacy as oleg
+    L, H, D, NH, NW, bits, gs = 32, 32, 128, 1024, 4096, 4, 64
+    cfg = ProductionCacheConfig(num_layers=L, num_heads=H, head_dim=D, hot_budget=NH, warm_budget=NW,
+                                warm_bits=bits, group_size=gs, warm_quantizer="minmax", max_hot_pages=NH // 16,
+                                device="cuda")
+    cache = ProductionCache(cfg)
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(7)
+
+    def rnd(n):
+        return torch.randn(H, n, D, generator=gen, device="cuda", dtype=torch.float16)
+
+    for lay in cache._layers:
+        lay._warm_k.quantize_and_append(rnd(NW))
+        lay._warm_v.quantize_and_append(rnd(NW))
+        lay.append_hot(rnd(NH), rnd(NH))
+    q = torch.randn(1, H, 1, D, generator=gen, device="cuda", dtype=torch.float16)
+
+    def calls():
+        return [cache.fused_attention(q, i) for i in range(L)]
+
+    calls()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    ms, wall_ms = _event_time(graph.replay, max(args.steps, 20), args.warmup)
+    us_layer = ms * 1e3 / L
+    qo = 2 * H * D * 2
+    hot = H * NH * D * 2 * 2
+    codes = H * NW * (D * bits // 8) * 2
+    meta = H * NW * (D // gs) * 2 * 2 * 2
+    alg = qo + hot + codes + meta
+    achieved = alg / (us_layer * 1e-6) / 1e9
+    # the reference's design: fp16 warm copy + hot copy into one buffer, then torch ops
+    bufs = []
+    for lay in cache._layers:
+        wk, wv = lay.get_warm_fp16()
+        kb = torch.empty(H, NW + NH, D, dtype=torch.float16, device="cuda")
+        vb = torch.empty_like(kb)
+        kb[:, :NW], vb[:, :NW] = wk, wv
+        bufs.append((kb, vb))
+    qt = q[0].transpose(-1, -2).contiguous()  # (H, D, 1): no transposed right operand
+
+    def ref_design():
+        for lay, (kb, vb) in zip(cache._layers, bufs):
+            kb[:, NW:] = lay._hot_k_contig[:, :NH]
+            vb[:, NW:] = lay._hot_v_contig[:, :NH]
+            p = torch.softmax(torch.matmul(kb, qt) * D ** -0.5, dim=1)  # (H, N, 1)
+            torch.matmul(p.transpose(1, 2).contiguous(), vb)
+
+    ref_ms, _ = _event_time(ref_design, max(args.steps, 20), args.warmup)
+    ref_bytes = hot * 2 + H * (NW + NH) * D * 2 * 2
+    res = {"metric": "ProductionCache.fused_attention us/layer + effective KV GB/s (% HBM peak), "
+                     "reference defaults (32 heads, 1024 hot + 4096 warm 4-bit), 1xMI355X",
+           "value": round((hot + codes + meta) / (us_layer * 1e-6) / 1e9, 2), "unit": "GB/s",
+           "higher_is_better": True, "dtype": "f16", "us_per_layer": round(us_layer, 3),
+           "config": {"workload": "production_decode_4k", "layers": L, "heads": H, "D": D, "n_hot": NH,
+                      "n_warm": NW, "bits": bits, "group_size": gs, "warm_quantizer": "minmax"},
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": recorded_traffic("production_decode_4k"),
+                        "kernel": "akv_decode_attn per layer (legacy arena warm tier, decode_fast_kernel LEG variant)",
+                        "algorithmic_bytes_per_launch": alg, "us_per_launch": round(us_layer, 3)},
+           "reference_design_gpu": {"us_per_layer": round(ref_ms * 1e3 / L, 3),
+                                    "bytes_per_layer": ref_bytes,
+                                    "what": "cached fp16 warm copy + hot copy, torch matmul/softmax/matmul"}}
+    if not args.no_cpu_baseline:
+        cores = len(os.sched_getaffinity(0))
+        lay = cache._layers[0]
+        host = [t.cpu().numpy() for a in (lay._warm_k, lay._warm_v) for t in (a.data, a.scales, a.zeros)]
+        hk = lay._hot_k_contig[:, :NH].float().cpu().numpy()
+        hv = lay._hot_v_contig[:, :NH].float().cpu().numpy()
+        qn = q[0, :, 0].float().cpu().numpy()
+        reps, t_cpu = 0, 0.0
+        with threadpool_limits(limits=cores):
+            while t_cpu < 3.0 or reps < 3:
+                t0 = time.perf_counter()
+                wk = oleg.arena_dequantize(*host[:3], bits, gs, D).astype(np.float32)
+                wv = oleg.arena_dequantize(*host[3:], bits, gs, D).astype(np.float32)
+                k, v = np.concatenate([wk, hk], axis=1), np.concatenate([wv, hv], axis=1)
+                sc = np.einsum("hd,hnd->hn", qn, k) * np.float32(D ** -0.5)
+                e = np.exp(sc - sc.max(axis=1, keepdims=True))
+                np.einsum("hn,hnd->hd", e / e.sum(axis=1, keepdims=True), v)
+                t_cpu += time.perf_counter() - t0
+                reps += 1
+        us = t_cpu / reps * 1e6
+        res["cpu_baseline"] = {"value": round(us, 1), "unit": "us per layer", "cores": cores, "kind": "port",
+                               "sample": f"layer 0 (arena dequant + fp32 attention), {reps} runs, "
+                                         f"{t_cpu:.1f} s on {cores} host threads"}
+    del cache, bufs
     return res
 
 

@@ -224,3 +224,17 @@ def test_full_size_qwen_32k_slice():
     ref, _ = oatt.mixed_attention_fp32(q[b:b + 1].cpu().numpy(), kh[b:b + 1].cpu().numpy(),
                                        vh[b:b + 1].cpu().numpy(), kd, vd, hot_first=False, return_weights=False)
     assert_close_attn(out[b:b + 1], ref)
+
+
+@pytest.mark.parametrize("B,Hkv,Nw,G", [(1, 1, 333, 128), (1, 1, 517, 64), (2, 2, 328, 128), (2, 2, 332, 64),
+                                        (2, 2, 333, 128), (1, 2, 301, 64)])
+def test_value_groups_64_128_ragged(B, Hkv, Nw, G):
+    """V groups of 64 / 128 channels (1 or 2 scale rows per token) with tier lengths
+    that end inside a 16-byte piece of the meta rows: the LDS-streamed kernel clears
+    the rows past the tier; per-(batch, head) tiers whose meta would not start on 16
+    bytes (odd lengths with B * Hkv > 1) run the general kernel."""
+    announce(f"decode G={G} B={B} Hkv={Hkv} Nw={Nw}")
+    q, kh, vh, w, kd, vd = _case(B, 4 * Hkv, Hkv, 128, 24, Nw, 4, 2, G=G, seed=12)
+    out = _run(q, kh, vh, w, hot_first=False)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False, return_weights=False)
+    assert_close_attn(out, ref)
