@@ -5,6 +5,7 @@ Module paths, names and signatures follow the reference package
 gfx950 kernels from libakv_hip.so.
 """
 from .affine_quantizer import AffineQuantConfig, AffineQuantizer
+from .baselines import KIVICache, KIVIConfig, KIVIFusedCache, KIVIFusedConfig, create_baseline
 from .bitpack import pack, unpack, packed_bytes
 from .drop_in import AKVCache, _PRESETS, select_demote_indices
 from .fused_attention import fused_int4_decode_attention, mixed_precision_decode_attention
@@ -25,6 +26,7 @@ __version__ = "0.1.0"
 
 __all__ = [
     "AffineQuantConfig", "AffineQuantizer", "pack", "unpack", "packed_bytes",
+    "KIVICache", "KIVIConfig", "KIVIFusedCache", "KIVIFusedConfig", "create_baseline",
     "AKVCache", "_PRESETS", "select_demote_indices",
     "fused_int4_decode_attention", "mixed_precision_decode_attention",
     "ImportanceConfig", "ImportanceScorer", "ScoringStrategy",

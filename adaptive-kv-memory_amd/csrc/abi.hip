@@ -195,7 +195,10 @@ int check_decode(const akv_decode_args *a) {
         if (w.bits_k != 2 && w.bits_k != 4 && w.bits_k != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", w.bits_k);
         if (!pow2(w.group_size) || w.group_size < 8) return fail(AKV_E_UNSUPPORTED, "group_size must be a power of two >= 8");
         if (w.meta_dtype < 0 || w.meta_dtype > 2) return fail(AKV_E_DTYPE, "bad meta dtype");
-        if (w.warm_heads != 1 && w.warm_heads != a->Hkv) return fail(AKV_E_SHAPE, "warm_heads must be 1 or Hkv");
+        if (w.warm_heads != 1 && w.warm_heads != a->Hkv && w.warm_heads != a->B * a->Hkv)
+            return fail(AKV_E_SHAPE, "warm_heads must be 1, Hkv or B * Hkv");
+        if (w.legacy_sym < 0 && w.token_stride > w.n_warm)
+            return fail(AKV_E_UNSUPPORTED, "symmetric-branch detection reads dense rows: force legacy_sym with a token stride");
         if (!w.k_codes || !w.v_codes || !w.k_scale || !w.k_zero || !w.v_scale || !w.v_zero)
             return fail(AKV_E_INVALID, "warm tier pointers missing");
         if (nw * (int64_t)a->D * 2 >= (int64_t)1 << 32) return fail(AKV_E_SHAPE, "warm tier per head exceeds 4 GiB");
@@ -586,8 +589,10 @@ int akv_dequant_unpack(const akv_dequant_args *a, void *stream) {
         p.n_out = w.n_out;
         p.k_oidx = w.k_oidx; p.v_oidx = w.v_oidx; p.k_odata = w.k_odata; p.v_odata = w.v_odata;
     } else if (w.kind == AKV_WARM_LEGACY) {
-        if (events || a->out_slot || (w.token_stride != 0 && w.token_stride != w.n_warm))
-            return fail(AKV_E_INVALID, "event blocks, token strides and output slots apply to the affine tier");
+        if (events || a->out_slot) return fail(AKV_E_INVALID, "event blocks and output slots apply to the affine tier");
+        if (w.token_stride != 0 && w.token_stride < w.n_warm) return fail(AKV_E_SHAPE, "token_stride < n_warm");
+        if (w.legacy_sym < 0 && w.token_stride > w.n_warm)
+            return fail(AKV_E_UNSUPPORTED, "symmetric-branch detection reads dense rows: force legacy_sym with a token stride");
         if (w.bits_k != w.bits_v) return fail(AKV_E_BITS, "legacy warm tier uses one width for K and V");
         if (w.bits_k != 2 && w.bits_k != 4 && w.bits_k != 8) return fail(AKV_E_BITS, "Unsupported bits: %d", w.bits_k);
         if (w.group_size < 1) return fail(AKV_E_SHAPE, "bad group_size");

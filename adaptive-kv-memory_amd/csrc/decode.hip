@@ -359,7 +359,8 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
     } else {
         // ----------------------------------------------------------- warm tiles
         const int unit = (WK == AKV_WARM_AFFINE) ? p.T : 16;  // tokens sharing K meta
-        const int64_t hw = (WK == AKV_WARM_AFFINE) ? bh : (p.warm_heads == 1 ? 0 : kvh);
+        // legacy: one tier shared by all, one per kv head, or one per (batch, kv head)
+        const int64_t hw = (WK == AKV_WARM_AFFINE) ? bh : (p.warm_heads == 1 ? 0 : p.warm_heads == p.Hkv ? kvh : bh);
         const int nwarm = (int)p.n_warm;
         const __amdgpu_buffer_rsrc_t rkc =
             make_rsrc((const unsigned char *)p.kc + hw * p.w_stride * p.kc_row, (uint32_t)(p.n_warm * p.kc_row));

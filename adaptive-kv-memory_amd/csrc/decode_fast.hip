@@ -335,9 +335,10 @@ void decode_fast_kernel(const DecodeParams p) {
     {
         const uint32_t nwu = (uint32_t)p.n_warm;
         // first token row of this (batch, kv-head)'s warm tier: dense per (batch, kv-head) for the
-        // block-affine layout; per warm head (shared by the batch, or by every head) and
-        // w_stride rows apart for the legacy layout
-        const int64_t wrow = LEG ? (int64_t)(p.warm_heads == 1 ? 0 : kvh) * p.w_stride : bh * p.n_warm;
+        // block-affine layout; for the legacy layout one tier shared by all, one per kv head
+        // (shared by the batch) or one per (batch, kv head), w_stride rows apart
+        const int64_t wrow =
+            LEG ? (p.warm_heads == 1 ? 0 : p.warm_heads == p.Hkv ? (int64_t)kvh : bh) * p.w_stride : bh * p.n_warm;
         R.kc = rsrc4((const unsigned char *)p.kc + wrow * L::KR, nwu * L::KR);
         R.vc = rsrc4((const unsigned char *)p.vc + wrow * L::VR, nwu * L::VR);
         // Per-token meta: with 4 groups a unit's rows are loaded a dword per lane, and every

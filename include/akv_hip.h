@@ -83,12 +83,13 @@ typedef struct akv_warm_desc {
     /* AKV_WARM_LEGACY */
     int32_t group_size;    /* group size along D */
     int32_t meta_dtype;    /* AKV_DT_* of scales / zeros */
-    int32_t warm_heads;    /* Hw: 1 or Hkv */
+    int32_t warm_heads;    /* Hw: 1 (shared), Hkv (per kv head) or, in decode, B * Hkv (per batch and kv head) */
     int32_t legacy_sym;    /* -1 detect, 0 asymmetric, 1 symmetric */
     /* token rows per warm head (LEGACY) or per (batch, kv-head) (AFFINE, dequant only) of
      * the codes, V meta and outlier values, >= n_warm; 0 = n_warm.  Lets a preallocated
      * store (PackedKVArena's [H][S][...] buffers, AKVLayer's growing tier) be read in
-     * place while only its first n_warm rows are filled. */
+     * place while only its first n_warm rows are filled.  A LEGACY tier with a stride above
+     * n_warm must force legacy_sym (0 or 1): the detection reads dense rows. */
     int64_t token_stride;
 } akv_warm_desc;
 

@@ -82,6 +82,35 @@ def test_decode_shape_checks():
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0
 
 
+def test_legacy_warm_heads_and_strides():
+    """A legacy tier is shared (1), per kv head (Hkv) or per (batch, kv head) (B * Hkv);
+    a token stride below n_warm is refused, and one above it needs a forced branch
+    (the symmetric-branch detection reads dense rows)."""
+    from akv import _native as nat
+    lib = nat.load()
+    a = nat.DecodeArgs()
+    a.abi_version = nat.ABI_VERSION
+    a.q_dtype = nat.DT_F16
+    a.B, a.Hq, a.Hkv, a.M, a.D = 3, 8, 4, 1, 128
+    a.q = a.out = 0x10000  # host-side checks only: never dereferenced
+    w = a.warm
+    w.kind = nat.WARM_LEGACY
+    w.bits_k = w.bits_v = 4
+    w.n_warm = 100
+    w.k_codes = w.v_codes = w.k_scale = w.k_zero = w.v_scale = w.v_zero = 0x20000
+    w.group_size, w.meta_dtype, w.legacy_sym = 64, nat.DT_F16, 0
+    for heads, ok in ((1, True), (4, True), (12, True), (3, False), (8, False)):
+        w.warm_heads = heads
+        assert (lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0) == ok, heads
+    w.warm_heads = 12
+    w.token_stride = 99
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1 and b"token_stride" in lib.akv_last_error()
+    w.token_stride = 128
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0
+    w.legacy_sym = -1
+    assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1 and b"force legacy_sym" in lib.akv_last_error()
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,M", [(1, 12, 2, 1), (8, 12, 2, 1), (4, 32, 32, 1), (2, 12, 2, 3), (3, 64, 2, 1),
                                           (2, 2, 2, 9)])
 def test_decode_counter_region(B, Hq, Hkv, M):

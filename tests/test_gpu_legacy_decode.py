@@ -6,7 +6,7 @@ Head_dim 128 with 2 / 4 bits, groups of 32 / 64 / 128 and fp16 scales runs the
 LDS-streamed kernel; 8 bits, head_dim 64 and bf16 / fp32 scales run the general
 split kernel.  Covered: the asymmetric branch and the symmetric one (all zero-points
 0, detected on the device, or forced), one warm tier shared by every batch element and
-head or one per head, grouped-query heads, ragged lengths, a token stride above the
+head, one per kv head or one per (batch, kv head), grouped-query heads, ragged lengths, a token stride above the
 warm length (an arena's capacity), hot tokens before or after the warm ones, and
 scales large enough that -1024 s overflows fp16 (the exact slow path)."""
 import numpy as np
@@ -62,13 +62,24 @@ def _ref(q, kh, vh, kd, vd, hot_first, warm_heads, B, Hkv):
     return ref
 
 
-CASES = [  # bits, gs, sym, warm_heads ("one" / "per"), B, Hq, Hkv, M, N, Nh, hot_first
+def _ref_full(q, kh, vh, kd, vd, hot_first, B, Hkv):
+    """Oracle attention with a warm tier per (batch, kv head): kd, vd (B, Hkv, N, D)."""
+    if kh is None:
+        kh = vh = np.zeros((B, Hkv, 0, q.shape[-1]), np.float16)
+    ref, _ = oatt.mixed_attention_fp32(q, kh, vh, kd.astype(np.float16), vd.astype(np.float16),
+                                       hot_first=hot_first, return_weights=False)
+    return ref
+
+
+CASES = [  # bits, gs, sym, warm tier ("one" shared / "per" kv head / "bh" per batch and kv head), B, Hq, Hkv, M, N, Nh, hot_first
     (4, 64, False, "per", 1, 32, 32, 1, 1000, 200, False),
     (4, 32, False, "one", 2, 8, 2, 1, 300, 40, True),
     (4, 128, True, "one", 2, 4, 4, 1, 517, 0, True),
     (2, 32, False, "per", 1, 8, 8, 1, 333, 16, False),
     (2, 64, True, "per", 3, 16, 4, 2, 250, 33, True),
     (2, 128, False, "one", 1, 12, 2, 1, 4096, 512, False),
+    (4, 128, False, "bh", 3, 8, 4, 1, 203, 64, False),
+    (2, 64, True, "bh", 2, 12, 2, 3, 450, 17, True),
 ]
 
 
@@ -77,15 +88,18 @@ def test_legacy_decode_matches_oracle(bits, gs, sym, wh, B, Hq, Hkv, M, N, Nh, h
     announce(f"legacy decode bits={bits} gs={gs} sym={sym} warm={wh} B={B} Hq={Hq} Hkv={Hkv} M={M} N={N} Nh={Nh}")
     rng = np.random.default_rng(bits * 100 + gs + N)
     D = 128
-    rows = 1 if wh == "one" else Hkv
+    rows = {"one": 1, "per": Hkv, "bh": B * Hkv}[wh]
     kp, ks, kz, kd = _tier(rng, rows, N, D, bits, gs, sym)
     vp, vs, vz, vd = _tier(rng, rows, N, D, bits, gs, sym)
     q = rng.standard_normal((B, Hq, M, D)).astype(np.float16)
     kh = rng.standard_normal((B, Hkv, Nh, D)).astype(np.float16) if Nh else None
     vh = rng.standard_normal((B, Hkv, Nh, D)).astype(np.float16) if Nh else None
     out = _run(q, kh, vh, ((kp, ks, kz), (vp, vs, vz)), bits, gs, N, D, rows, Hkv, hot_first)
-    assert_close_attn(out, _ref(q, kh, vh, kd if rows > 1 else kd[0], vd if rows > 1 else vd[0], hot_first, rows,
-                                B, Hkv))
+    if wh == "bh":  # (B * Hkv, N, D) -> (B, Hkv, N, D)
+        ref = _ref_full(q, kh, vh, kd.reshape(B, Hkv, N, D), vd.reshape(B, Hkv, N, D), hot_first, B, Hkv)
+    else:
+        ref = _ref(q, kh, vh, kd if rows > 1 else kd[0], vd if rows > 1 else vd[0], hot_first, rows, B, Hkv)
+    assert_close_attn(out, ref)
 
 
 @pytest.mark.parametrize("sym", [0, 1])
