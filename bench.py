@@ -22,7 +22,8 @@ reference CPU path beside it), llama7b_decode_16k (MHA, K4/V2 with outlier
 channels), llama3_demote_64k (select + gather + quantize + pack, 3-bit),
 llama70b_prefill_128k (MFMA chunked prefill) and production_decode_4k
 (ProductionCache.fused_attention over the 4-bit arenas at the cache's default
-sizes, with the reference's torch design timed beside it).  --workload NAME
+sizes, with the reference's torch design timed beside it) and kivi_decode_4k
+(the KIVI baseline's attention at the same sizes, 2 bits).  --workload NAME
 prints one of them on its own line instead.
 
 The roofline is taken on the attention-only replay (per layer: one launch of
@@ -116,7 +117,7 @@ def main():
                     help="end with one device copy of 256 MiB (reference dispatch for counter runs)")
     ap.add_argument("--workload", default="qwen_decode_32k",
                     choices=["qwen_decode_32k", "llama7b_decode_16k", "llama70b_prefill_128k", "llama3_demote_64k",
-                             "qwen_decode_4k", "production_decode_4k"],
+                             "qwen_decode_4k", "production_decode_4k", "kivi_decode_4k"],
                     help="the headline decode step (default; the other workloads are summarised in its "
                          "'workloads' field), or one other workload on its own line")
     ap.add_argument("--no-other-workloads", action="store_true",
@@ -142,7 +143,7 @@ def main():
     if args.workload != "qwen_decode_32k":
         fn = {"llama70b_prefill_128k": bench_prefill, "llama3_demote_64k": bench_demote,
               "llama7b_decode_16k": bench_decode_mha, "qwen_decode_4k": bench_c1,
-              "production_decode_4k": bench_production}[args.workload]
+              "production_decode_4k": bench_production, "kivi_decode_4k": bench_kivi}[args.workload]
         print(json.dumps(fn(args)), flush=True)
         return
 
@@ -241,7 +242,7 @@ def main():
 
 
 SUMMARY_KEYS = ("metric", "value", "unit", "ms_per_call", "us_per_layer", "ms_quantize_only", "roofline",
-                "cpu_baseline", "config", "gpu_us_per_layer")
+                "cpu_baseline", "config", "gpu_us_per_layer", "reference_design_gpu")
 
 
 def other_workloads(args):
@@ -252,7 +253,7 @@ def other_workloads(args):
     out = {}
     for name, fn in (("qwen_decode_4k", bench_c1), ("llama7b_decode_16k", bench_decode_mha),
                      ("llama3_demote_64k", bench_demote), ("llama70b_prefill_128k", bench_prefill),
-                     ("production_decode_4k", bench_production)):
+                     ("production_decode_4k", bench_production), ("kivi_decode_4k", bench_kivi)):
         print(f"[bench] workload {name}", file=sys.stderr, flush=True)
         try:
             r = fn(args)
@@ -432,6 +433,102 @@ def bench_production(args):
     return res
 
 
+def bench_kivi(args):
+    """KIVIFusedCache.fused_attention (akv/baselines.py:426-510 with this build's attention
+    leg) at the production cache's sizes: 32 layers, 32 heads, head_dim 128, 4096 tokens
+    quantized at 2 bits in groups of 128 plus the 128-token residual window, one query
+    token; the 32 layers' calls captured in one graph.  Beside it, the reference's use
+    of the baseline on the same GPU: the float16 view ``update`` returns (the working
+    copy concatenated with the residual) attended by matmul / softmax / matmul."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+    from akv.baselines import KIVIFusedCache, KIVIFusedConfig
+    from oracle.kivi import kivi_dequantize
+    from oracle import legacy as oleg
+    L, H, D, NQ, RES, bits, gs = 32, 32, 128, 4096, 128, 2, 128
+    cache = KIVIFusedCache(KIVIFusedConfig(key_bits=bits, value_bits=bits, group_size=gs, residual_length=RES))
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(11)
+    views = []
+    for layer in range(L):
+        k = torch.randn(1, H, NQ + RES, D, generator=gen, device="cuda", dtype=torch.float16)
+        v = torch.randn(1, H, NQ + RES, D, generator=gen, device="cuda", dtype=torch.float16)
+        views.append(cache.update(k, v, layer))
+        del k, v
+    q = torch.randn(1, H, 1, D, generator=gen, device="cuda", dtype=torch.float16)
+
+    def calls():
+        return [cache.fused_attention(q, i) for i in range(L)]
+
+    calls()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    ms, _ = _event_time(graph.replay, max(args.steps, 20), args.warmup)
+    us_layer = ms * 1e3 / L
+    qo = 2 * H * D * 2
+    hot = H * RES * D * 2 * 2
+    codes = H * NQ * (D * bits // 8) * 2
+    meta = H * NQ * (D // gs) * 2 * 2 * 2
+    alg = qo + hot + codes + meta
+    achieved = alg / (us_layer * 1e-6) / 1e9
+    qt = q[0].transpose(-1, -2).contiguous()  # (H, D, 1): no transposed right operand
+
+    def ref_design():  # the view update returns, then the attention a model runs on it
+        for layer in range(L):
+            kv, vv = cache._get_full_kv(layer)
+            p = torch.softmax(torch.matmul(kv[0], qt) * D ** -0.5, dim=1)
+            torch.matmul(p.transpose(1, 2).contiguous(), vv[0])
+
+    ref_ms, _ = _event_time(ref_design, max(args.steps, 20), args.warmup)
+    res = {"metric": "KIVIFusedCache.fused_attention us/layer + effective KV GB/s (% HBM peak), 32 heads, "
+                     "4096 tokens at 2 bits + 128 residual, 1xMI355X",
+           "value": round((hot + codes + meta) / (us_layer * 1e-6) / 1e9, 2), "unit": "GB/s",
+           "higher_is_better": True, "dtype": "f16", "us_per_layer": round(us_layer, 3),
+           "config": {"workload": "kivi_decode_4k", "layers": L, "heads": H, "D": D, "quantized": NQ,
+                      "residual": RES, "bits": bits, "group_size": gs},
+           "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": recorded_traffic("kivi_decode_4k"),
+                        "kernel": "akv_decode_attn per layer (legacy per-(batch, head) tier, decode_fast_kernel LEG "
+                                  "variant)",
+                        "algorithmic_bytes_per_launch": alg, "us_per_launch": round(us_layer, 3)},
+           "reference_design_gpu": {"us_per_layer": round(ref_ms * 1e3 / L, 3),
+                                    "what": "float16 working copy + residual concatenated, torch "
+                                            "matmul/softmax/matmul"}}
+    if not args.no_cpu_baseline:
+        cores = len(os.sched_getaffinity(0))
+        t_k, t_v = cache._quant_keys[0], cache._quant_values[0]
+        n = t_k.n
+        host = [(np.ascontiguousarray(t.codes[:, :n].cpu().numpy()), t.sc[:, :n].cpu().numpy(),
+                 t.ze[:, :n].cpu().numpy()) for t in (t_k, t_v)]
+        rk = cache._residual_keys[0][0].float().cpu().numpy()
+        rv = cache._residual_values[0][0].float().cpu().numpy()
+        qn = q[0, :, 0].float().cpu().numpy()
+        reps, t_cpu = 0, 0.0
+        with threadpool_limits(limits=cores):
+            while t_cpu < 3.0 or reps < 3:
+                t0 = time.perf_counter()
+                kv = []
+                for c, s_, z_ in host:
+                    u = oleg.arena_unpack(c, bits, D)
+                    kv.append(kivi_dequantize(u.astype(np.uint8).reshape(H * n, 1, D), s_.reshape(H * n, 1),
+                                              z_.reshape(H * n, 1), (1, H, n, D))[0].astype(np.float32))
+                k = np.concatenate([kv[0], rk], axis=1)
+                v = np.concatenate([kv[1], rv], axis=1)
+                sc = np.einsum("hd,hnd->hn", qn, k) * np.float32(D ** -0.5)
+                e = np.exp(sc - sc.max(axis=1, keepdims=True))
+                np.einsum("hn,hnd->hd", e / e.sum(axis=1, keepdims=True), v)
+                t_cpu += time.perf_counter() - t0
+                reps += 1
+        res["cpu_baseline"] = {"value": round(t_cpu / reps * 1e6, 1), "unit": "us per layer", "cores": cores,
+                               "kind": "port", "sample": f"layer 0 (dequant + fp32 attention), {reps} runs, "
+                                                         f"{t_cpu:.1f} s on {cores} host threads"}
+    del cache, views
+    return res
+
+
 def recorded_traffic(workload, phase="all"):
     """HBM bytes per launch of the workload's dominant kernel, from the counter runs
     summarised in TRAFFIC_FILE (None when that file has no entry)."""
@@ -470,7 +567,14 @@ def _workload_dispatches(disp, steps, warmup):
     L = 28
     n_rep = (warmup + steps) * L
     for key, ds in groups.items():
-        if key.startswith("decode_fast_kernel<3, 3,"):
+        legacy = key.startswith("decode_fast_kernel") and key.endswith("true>")  # the LEG variant
+        if legacy and key.startswith("decode_fast_kernel<4, 4,"):
+            out[("production_decode_4k", "all")] = (key, ds)
+        elif legacy and key.startswith("decode_fast_kernel<2, 2,"):
+            out[("kivi_decode_4k", "all")] = (key, ds)
+        elif legacy:
+            continue
+        elif key.startswith("decode_fast_kernel<3, 3,"):
             out[("qwen_decode_32k", "attention_only")] = (key, ds[-n_rep:])
             out[("qwen_decode_32k", "with_importance")] = (key, ds[-2 * n_rep:-n_rep])
         elif key.startswith("decode_fast_kernel<4, 4,"):
