@@ -86,3 +86,67 @@ def test_two_layers_in_one_graph():
         torch.cuda.synchronize()
         for c, ref in zip(calls, refs):
             assert_close_attn(c.out, ref)
+
+
+def _graph_matches_eager(calls, n_replays=4):
+    """Capture `calls` (a list of zero-argument callables returning tensors) in one graph;
+    after every replay, with eager work between, each output equals an eager call's."""
+    eager_first = [c() for c in calls]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [c() for c in calls]
+    torch.cuda.synchronize()
+    scratch = torch.zeros(1 << 20, device="cuda")
+    for r in range(n_replays):
+        g.replay()
+        eager = [c() for c in calls]
+        scratch.add_(1.0)
+        torch.cuda.synchronize()
+        for i, (o, e) in enumerate(zip(outs, eager)):
+            torch.testing.assert_close(o, e, atol=2e-4, rtol=2e-3, msg=f"replay {r}, call {i}")
+    return outs, eager_first
+
+
+def test_production_fused_attention_in_a_graph():
+    """ProductionCache.fused_attention over two layers captured once: the layers' decode
+    workspaces are reused, so the graph holds only the decode launches."""
+    from akv.production_cache import ProductionCache, ProductionCacheConfig
+    from oracle.production import ProductionCacheOracle
+    announce("ProductionCache.fused_attention graph replays")
+    cfg = ProductionCacheConfig(num_layers=2, num_heads=8, head_dim=128, hot_budget=64, warm_budget=512, warm_bits=4,
+                                group_size=64, warm_quantizer="minmax", max_hot_pages=16, batch_migration_size=64,
+                                device="cuda")
+    pc = ProductionCache(cfg)
+    orc = ProductionCacheOracle(2, 8, 128, 64, 512, 4, 64, batch_migration_size=64, decay=cfg.importance_decay)
+    rng = np.random.default_rng(7)
+    for layer in range(2):
+        for n in (200, 1, 1):
+            k = rng.standard_normal((8, n, 128)).astype(np.float16).astype(np.float32)
+            v = rng.standard_normal((8, n, 128)).astype(np.float16).astype(np.float32)
+            pc.update(to_dev(k, torch.float16), to_dev(v, torch.float16), layer)
+            orc.update(k, v, layer)
+    q = rng.standard_normal((1, 8, 1, 128)).astype(np.float32)
+    dq = to_dev(q, torch.float16)
+    outs, _ = _graph_matches_eager([lambda: pc.fused_attention(dq, 0), lambda: pc.fused_attention(dq, 1)])
+    for layer in range(2):
+        assert_close_attn(outs[layer], orc.attention(q, layer))
+
+
+def test_kivi_fused_attention_in_a_graph():
+    from akv.baselines import KIVIFusedCache, KIVIFusedConfig
+    from oracle.kivi import KIVIOracle
+    announce("KIVIFusedCache.fused_attention graph replays")
+    cache = KIVIFusedCache(KIVIFusedConfig(key_bits=2, value_bits=2, group_size=128, residual_length=32))
+    orc = KIVIOracle(2, 2, 128, 32, fused=True)
+    rng = np.random.default_rng(8)
+    k = rng.standard_normal((2, 4, 400, 128)).astype(np.float16).astype(np.float32)
+    v = rng.standard_normal((2, 4, 400, 128)).astype(np.float16).astype(np.float32)
+    cache.update(to_dev(k, torch.float16), to_dev(v, torch.float16), 0)
+    ok, ov = orc.update(k, v, 0)
+    q = rng.standard_normal((2, 8, 1, 128)).astype(np.float32)
+    dq = to_dev(q, torch.float16)
+    outs, _ = _graph_matches_eager([lambda: cache.fused_attention(dq, 0)])
+    ref, _ = oatt.attention_fp32(q.astype(np.float16), ok.astype(np.float16), ov.astype(np.float16),
+                                 return_weights=False)
+    assert_close_attn(outs[0], ref)
