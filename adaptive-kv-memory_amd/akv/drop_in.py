@@ -272,6 +272,79 @@ class _EventTier:
         self.B = self.t["kc"].shape[0]
 
 
+class _HeadBitsTier:
+    """The packed warm tier when each head has its own code width (a calibration's
+    ``per_head_bits``, akv/drop_in.py:315-374): one ``_EventTier`` per width over that
+    width's heads, each (batch element, head) its own row -- the reference quantizes
+    every head with its own AffineQuantizer of that width (the pool keyed by bits), so
+    keys are per channel over the event's tokens of that head and the outlier channels
+    are chosen per head.  Same interface as ``_EventTier``."""
+
+    def __init__(self, B, H, D, per_head_bits, dev):
+        self.B, self.H, self.D, self.dev = B, H, D, dev
+        self.n = 0
+        self.groups = []  # [bits, head indices on the device, _EventTier or None]
+        for bits in sorted(set(per_head_bits)):
+            heads = [h for h, b in enumerate(per_head_bits) if b == bits]
+            self.groups.append([bits, torch.tensor(heads, dtype=torch.long, device=dev), None])
+
+    def demote(self, hk, hv, idx, outlier_fraction, positions) -> int:
+        """Quantize hot tokens ``idx`` of every head with its width as one event; returns
+        the measured packed bytes (codes + scale + zero of K and V, per head)."""
+        B, _, _, D = hk.shape
+        n = idx.numel()
+        packed = 0
+        for g in self.groups:
+            bits, heads, tier = g
+            hs = heads.numel()
+            k = hk.index_select(1, heads).index_select(2, idx).reshape(B * hs, 1, n, D)
+            v = hv.index_select(1, heads).index_select(2, idx).reshape(B * hs, 1, n, D)
+            w = quantize_kv(k, v, bits, bits, block_t=max(n, 1), group_v=D, outlier_fraction=outlier_fraction)
+            if tier is None:
+                g[2] = tier = _EventTier(B * hs, 1, D, bits, bits, w.n_out, self.dev)
+            tier.append(w, positions)
+            packed += (w.k_codes.nbytes + w.k_scale.nbytes + w.k_zero.nbytes
+                       + w.v_codes.nbytes + w.v_scale.nbytes + w.v_zero.nbytes)
+        self.n += n
+        return packed
+
+    def resident_bytes(self) -> int:
+        return sum(g[2].resident_bytes() for g in self.groups if g[2] is not None)
+
+    def dequantize_into(self, out_k: torch.Tensor, out_v: torch.Tensor, slots: bool = True):
+        rows = out_k.shape[2]
+        for bits, heads, tier in self.groups:
+            hs = heads.numel()
+            tk = torch.empty(self.B * hs, 1, rows, self.D, dtype=out_k.dtype, device=out_k.device)
+            tv = torch.empty_like(tk)
+            tier.dequantize_into(tk, tv, slots)
+            out_k.index_copy_(1, heads, tk.view(self.B, hs, rows, self.D))
+            out_v.index_copy_(1, heads, tv.view(self.B, hs, rows, self.D))
+
+    def take(self, idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        n = idx.numel()
+        k = torch.empty(self.B, self.H, n, self.D, dtype=torch.float16, device=self.dev)
+        v = torch.empty_like(k)
+        for bits, heads, tier in self.groups:
+            tk, tv = tier.take(idx)
+            k.index_copy_(1, heads, tk.view(self.B, heads.numel(), n, self.D))
+            v.index_copy_(1, heads, tv.view(self.B, heads.numel(), n, self.D))
+        return k, v
+
+    def keep(self, keep_mask: torch.Tensor):
+        for g in self.groups:
+            g[2].keep(keep_mask)
+        self.n = int(keep_mask.sum())
+
+    def index_batch(self, beam_idx: torch.Tensor):
+        beam_idx = beam_idx.to(self.dev)
+        for g in self.groups:
+            hs = g[1].numel()
+            rows = (beam_idx.unsqueeze(1) * hs + torch.arange(hs, device=self.dev)).flatten()
+            g[2].index_batch(rows)
+        self.B = beam_idx.numel()
+
+
 class AKVLayer:
     """One layer of the drop-in cache (akv/drop_in.py:169-873) with the warm tier
     kept packed on the device.
@@ -300,9 +373,10 @@ class AKVLayer:
     leave the packed tier.
 
     Each batch element is its own quantizer call over (H, n, D) -- the
-    reference's call on ``k.squeeze(0)`` at batch 1.  Per-head bit widths are not
-    built: ``per_head_bits`` must be unset (or of another head count, where the
-    reference falls back to the global widths)."""
+    reference's call on ``k.squeeze(0)`` at batch 1.  With ``per_head_bits`` naming
+    a width for every head (a calibration's), each (batch element, head) is its own
+    call at its width (``_HeadBitsTier``); of another head count, the global widths
+    apply, as in the reference."""
 
     def __init__(self, warm_bits: int = 3, hot_budget: int = 128, group_size: int = 64, protect: bool = False,
                  enable_promotion: bool = True, promotion_threshold: float = 0.05,
@@ -410,14 +484,19 @@ class AKVLayer:
         idx = select_demote_indices(self._importance, n_demote, hot_len, self.hot_budget, device=dev)
         idx_host = idx.cpu()
         positions = self._hot_positions[idx_host]
-        w = quantize_kv(hk, hv, self.warm_key_bits, self.warm_value_bits, block_t=max(n_demote, 1), group_v=D,
-                        outlier_fraction=self.outlier_fraction, sel=idx.unsqueeze(0).expand(B, n_demote))
-        if self._warm is None:
-            self._warm = _EventTier(B, H, D, self.warm_key_bits, self.warm_value_bits, w.n_out, dev)
-        self._warm.append(w, positions.to(dev))
-        # measure_packed_bytes per batch element: packed codes + fp16 scale and zero, K and V
-        self._warm_bytes_packed += (w.k_codes.nbytes + w.k_scale.nbytes + w.k_zero.nbytes
-                                    + w.v_codes.nbytes + w.v_scale.nbytes + w.v_zero.nbytes)
+        if self.per_head_bits and len(self.per_head_bits) == H:
+            if self._warm is None:
+                self._warm = _HeadBitsTier(B, H, D, self.per_head_bits, dev)
+            self._warm_bytes_packed += self._warm.demote(hk, hv, idx, self.outlier_fraction, positions.to(dev))
+        else:
+            w = quantize_kv(hk, hv, self.warm_key_bits, self.warm_value_bits, block_t=max(n_demote, 1), group_v=D,
+                            outlier_fraction=self.outlier_fraction, sel=idx.unsqueeze(0).expand(B, n_demote))
+            if self._warm is None:
+                self._warm = _EventTier(B, H, D, self.warm_key_bits, self.warm_value_bits, w.n_out, dev)
+            self._warm.append(w, positions.to(dev))
+            # measure_packed_bytes per batch element: packed codes + fp16 scale and zero, K and V
+            self._warm_bytes_packed += (w.k_codes.nbytes + w.k_scale.nbytes + w.k_zero.nbytes
+                                        + w.v_codes.nbytes + w.v_scale.nbytes + w.v_zero.nbytes)
         self._warm_positions = positions if self._warm_positions is None else torch.cat([self._warm_positions,
                                                                                          positions])
         self._warm_len += n_demote
@@ -443,8 +522,6 @@ class AKVLayer:
             self._total_len += N
             self.keys, self.values = self._hot_keys, self._hot_values
             return self._hot_keys, self._hot_values
-        if self.per_head_bits and len(self.per_head_bits) == H:
-            raise NotImplementedError("per-head bit widths are not built for the packed warm tier")
         self._append_hot(key_states, value_states, new_positions)
         self._total_len += N
         self._step += 1

@@ -29,7 +29,9 @@ Per call with (B, H, N, D) keys / values:
     float32) sorted by position (:762-787); protected layers keep every token
     hot and return the hot tier.
 Each batch element is one AffineQuantizer call over (H, n, D): the reference
-calls it once on ``k.squeeze(0)``, which is that call at batch 1.
+calls it once on ``k.squeeze(0)``, which is that call at batch 1.  With
+``per_head_bits`` of H entries each (batch element, head) is one call at that
+head's width (akv/drop_in.py:315-374).
 
 This module is test infrastructure: only the tests, the smoke check and the
 benchmark's CPU-baseline leg use it, as the checker.
@@ -62,7 +64,7 @@ class AKVLayerOracle:
 
     def __init__(self, warm_bits=3, hot_budget=128, protect=False, adaptive_hot_frac=0.0,
                  warm_key_bits=None, warm_value_bits=None, outlier_fraction=0.0, enable_promotion=False,
-                 promotion_threshold=0.05, enable_promotion_proxy=False, proxy_decay=0.7):
+                 promotion_threshold=0.05, enable_promotion_proxy=False, proxy_decay=0.7, per_head_bits=None):
         self.enable_promotion = enable_promotion
         self.promotion_threshold = promotion_threshold
         self.enable_promotion_proxy = enable_promotion_proxy
@@ -76,6 +78,7 @@ class AKVLayerOracle:
         self.warm_key_bits = warm_key_bits or warm_bits
         self.warm_value_bits = warm_value_bits or warm_bits
         self.outlier_fraction = outlier_fraction
+        self.per_head_bits = list(per_head_bits) if per_head_bits is not None else None
         self.hot_k = self.hot_v = None
         self.hot_pos = None
         self.warm_k = self.warm_v = None
@@ -194,6 +197,18 @@ class AKVLayerOracle:
             wv = np.zeros((B, H, n, D), np.float16)
             per_b = []
             for b in range(B):
+                if self.per_head_bits and len(self.per_head_bits) == H:
+                    # one quantizer call per head at its width (akv/drop_in.py:349-374)
+                    heads = []
+                    for h, bits in enumerate(self.per_head_bits):
+                        qk = oaff.quantize_keys(dk[b, h:h + 1], bits, self.outlier_fraction, dt=dt)
+                        qv = oaff.quantize_values(dv[b, h:h + 1], bits, self.outlier_fraction, dt=dt)
+                        wk[b, h] = oaff.dequantize_keys(qk)[0]
+                        wv[b, h] = oaff.dequantize_values(qv)[0]
+                        self.warm_bytes_packed += packed_bytes(qk) + packed_bytes(qv)
+                        heads.append((qk, qv))
+                    per_b.append(heads)
+                    continue
                 qk = oaff.quantize_keys(dk[b], self.warm_key_bits, self.outlier_fraction, dt=dt)
                 qv = oaff.quantize_values(dv[b], self.warm_value_bits, self.outlier_fraction, dt=dt)
                 wk[b] = oaff.dequantize_keys(qk)

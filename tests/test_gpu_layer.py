@@ -126,14 +126,51 @@ def test_getitem_and_reorder_cache():
     _same(fk.flip(0), ok, "view after reorder_cache([1, 0])")
 
 
-def test_per_head_bits_are_refused():
-    from akv.drop_in import AKVLayer
-    announce("AKVLayer refuses per-head widths")
+@pytest.mark.parametrize("of", [0.0, 0.02])
+def test_per_head_bits_match_oracle(of):
+    """Calibrated per-head widths: each (batch element, head) is quantized at its own
+    width with its own outlier channels; views, positions, packed bytes and the warm
+    view in demotion order match the oracle, through a promotion from attention
+    weights and a reorder_cache."""
+    from akv.drop_in import AKVCache, AKVLayer
+    announce(f"AKVLayer per-head widths, outliers {of}")
+    B, H, D, bits = 2, 4, 128, [2, 4, 3, 4]
+    layer = AKVLayer(warm_bits=3, hot_budget=48, outlier_fraction=of, enable_promotion=True,
+                     enable_promotion_proxy=False, per_head_bits=bits)
+    orc = AKVLayerOracle(warm_bits=3, hot_budget=48, outlier_fraction=of, enable_promotion=True,
+                         enable_promotion_proxy=False, per_head_bits=bits)
+    _run(layer, orc, B, H, D, torch.float16, [200] + [1] * 5 + [30, 1], seed=31)
+    wk, wv = layer.warm_view()
+    _same(wk, orc.warm_k, "warm view K (demotion order)")
+    _same(wv, orc.warm_v, "warm view V")
+    # promotion from attention weights takes tokens out of every width's tier
+    rng = np.random.default_rng(32)
+    n_all = orc.warm_len + orc.hot_k.shape[2] + 1
+    aw = np.full((B, H, 1, n_all), 0.001, np.float32)
+    aw[..., [1, 7, 30]] = [0.3, 0.2, 0.5]
+    k, kh = _tokens(rng, B, H, 1, D, torch.float16)
+    v, vh = _tokens(rng, B, H, 1, D, torch.float16)
+    fk, fv = layer.update(k, v, {"attention_weights": to_dev(aw)})
+    ok, ov, _ = orc.update(kh, vh, attention_weights=aw)
+    _same(fk, ok, "K view after the promotion")
+    _same(fv, ov, "V view after the promotion")
+    assert orc.promoted_total == 3 and layer._warm_bytes_packed == orc.warm_bytes_packed
+    # another head count: the global widths apply (the reference's fallback)
     k = torch.zeros(1, 2, 4, 128, dtype=torch.float16, device="cuda")
-    with pytest.raises(NotImplementedError):
-        AKVLayer(hot_budget=2, enable_promotion=False, per_head_bits=[2, 4]).update(k, k)
-    # another head count: the reference falls back to the global widths
     AKVLayer(hot_budget=2, enable_promotion=False, per_head_bits=[2, 4, 4]).update(k, k)
+    # reorder_cache over the per-width tiers
+    cache = AKVCache(warm_bits=3, hot_budget=16, enable_promotion=False)
+    cache._calibration_per_head_bits = {0: [2, 4]}
+    orc2 = AKVLayerOracle(warm_bits=3, hot_budget=16, per_head_bits=[2, 4])
+    k, kh = _tokens(rng, 2, 2, 60, D, torch.float16)
+    v, vh = _tokens(rng, 2, 2, 60, D, torch.float16)
+    cache.update(k, v, 0)
+    orc2.update(kh, vh)
+    cache.reorder_cache(torch.tensor([1, 0], device="cuda"))
+    k2, kh2 = _tokens(rng, 2, 2, 1, D, torch.float16)
+    fk, _ = cache.update(k2, k2, 0)
+    ok, _, _ = orc2.update(kh2[::-1].copy(), kh2[::-1].copy())
+    _same(fk.flip(0), ok, "view after reorder_cache([1, 0]) with per-head widths")
 
 
 def test_promotion_from_attention_weights():
