@@ -126,7 +126,7 @@ EXPORTS = (
     "akv_decode_workspace_bytes", "akv_decode_counter_bytes", "akv_decode_attn", "akv_decode_attn_noalloc",
     "akv_quant_pack", "akv_dequant_unpack",
     "akv_bitpack", "akv_bitunpack", "akv_importance_update",
-    "akv_prefill_workspace_bytes", "akv_prefill_attn", "akv_select_demote",
+    "akv_prefill_workspace_bytes", "akv_prefill_attn", "akv_select_demote", "akv_stream_read",
 )
 STRUCTS = (WarmDesc, DecodeArgs, QuantArgs, DequantArgs, ImportanceArgs, PrefillArgs)
 
@@ -171,6 +171,8 @@ def load() -> ctypes.CDLL:
     lib.akv_prefill_attn.argtypes = [ctypes.POINTER(PrefillArgs), _vp]
     lib.akv_select_demote.restype = ctypes.c_int
     lib.akv_select_demote.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]
+    lib.akv_stream_read.restype = ctypes.c_int
+    lib.akv_stream_read.argtypes = [_vp, _i64, _vp, _vp]
     if lib.akv_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH} has ABI {lib.akv_abi_version()}, expected {ABI_VERSION}")
     for i, st in enumerate(STRUCTS):

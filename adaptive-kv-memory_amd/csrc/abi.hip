@@ -685,6 +685,15 @@ int akv_prefill_attn(const akv_prefill_args *a, void *stream) {
     return ok();
 }
 
+int akv_stream_read(const void *data, int64_t bytes, uint32_t *sink, void *stream) {
+    if (bytes < 0 || bytes % 16) return fail(AKV_E_SHAPE, "bytes must be a non-negative multiple of 16");
+    if (bytes > 0 && (!data || !sink)) return fail(AKV_E_INVALID, "null pointer");
+    if (bytes > 0 && !aligned16(data)) return fail(AKV_E_ALIGN, "data must be 16-byte aligned");
+    hipError_t e = akv::stream_read_launch(data, bytes, sink, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "stream read launch");
+    return ok();
+}
+
 int akv_select_demote(const float *scores, int64_t rows, int64_t len, int64_t n_demote, int32_t protect_first,
                       int32_t protect_last, int64_t *out, void *stream) {
     if (rows < 0 || len < 0 || n_demote < 0) return fail(AKV_E_SHAPE, "negative size");

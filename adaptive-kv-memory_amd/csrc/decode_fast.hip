@@ -14,7 +14,7 @@
 //
 // Work split: a 1-D grid over (split, kv-head, batch * row-chunk), renumbered
 // so that each XCD gets a contiguous run of items; a workgroup of 12 waves (8
-// for OUT) owns one (batch, kv-head, row chunk of 16 query rows) and one token
+// for OUT > 1) owns one (batch, kv-head, row chunk of 16 query rows) and one token
 // range: warm 32-token units first, then hot 16-token tiles (each two items:
 // its K and its V half).  A wave takes its first item by its index and the
 // next ones from a workgroup counter in LDS, through a private ring of NS LDS
@@ -79,8 +79,10 @@ constexpr int kD = 128;
 constexpr int kWaves = AKV_FAST_WAVES;  // waves per workgroup (one workgroup per CU, 3 per SIMD)
 constexpr int kUnit = 32;               // warm tokens per ring slot
 constexpr int kNS = AKV_FAST_NS;        // ring slots per wave (deeper rings only lengthen the tail)
-// With outlier channels the kernel holds more state per lane: 8 waves (2 per
-// SIMD, twice the registers each) with 3 ring slots each.
+// OUT selects the outlier-channel variant: 0 none; 1 exactly one channel per
+// block (the one-channel paths only: 147-156 VGPRs, so 12 waves with 2 slots
+// like OUT = 0); kMaxOut up to 4 channels, whose general corrections hold more
+// state per lane: 8 waves (2 per SIMD, twice the registers each) with 3 slots.
 #ifndef AKV_FAST_WAVES_OUT
 #define AKV_FAST_WAVES_OUT 8
 #endif
@@ -88,8 +90,8 @@ constexpr int kNS = AKV_FAST_NS;        // ring slots per wave (deeper rings onl
 #define AKV_FAST_NS_OUT 3
 #endif
 constexpr int kWavesOut = AKV_FAST_WAVES_OUT, kNSOut = AKV_FAST_NS_OUT;
-template <bool OUT> struct FastCfg {
-    static constexpr int NW = OUT ? kWavesOut : kWaves, NS = OUT ? kNSOut : kNS;
+template <int OUT> struct FastCfg {
+    static constexpr int NW = OUT > 1 ? kWavesOut : kWaves, NS = OUT > 1 ? kNSOut : kNS;
 };
 constexpr int kLdsCap = 160 * 1024;  // LDS of one CU
 constexpr int kKmetaBytes = 3 * 4 * 16 * 4;  // [s | n | z][group][pair] u32
@@ -99,7 +101,7 @@ constexpr int kAccRow = kD + 4;      // fp32 row of the end-of-split merge in LD
                                      // wave's 64 row/chunk writes over the banks)
 constexpr int kMaxOut = 4;            // outlier channels per block the fast kernel takes
 constexpr int kOutBytes = 2 * (kUnit * kMaxOut * 2) + 2 * 32;  // K/V outlier values + K/V indices
-template <int BK, int BV, int NG, bool OUT, bool LEG>
+template <int BK, int BV, int NG, int OUT, bool LEG>
 struct WarmLayout {
     static constexpr int KR = 16 * BK, VR = 16 * BV;  // packed row bytes (D = 128)
     static constexpr int KCB = kUnit * KR, VCB = kUnit * VR;
@@ -125,7 +127,7 @@ struct WarmRes {
     u4 ko, vo, ki, vi;  // outlier values and indices
 };
 
-template <int BK, int BV, int NG, bool OUT, bool LEG>
+template <int BK, int BV, int NG, int OUT, bool LEG>
 __device__ __forceinline__ void issue_warm(const WarmRes &R, unsigned char *slot, int lane, int u, int T, int tshift,
                                            int n_out) {
     using L = WarmLayout<BK, BV, NG, OUT, LEG>;
@@ -253,7 +255,7 @@ __device__ __forceinline__ void wait_younger(int nw, int nh) {
     else wait_vm<0>();
 }
 
-template <int BK, int BV, int NG, int NS, bool OUT, bool LEG>
+template <int BK, int BV, int NG, int NS, int OUT, bool LEG>
 __global__ __launch_bounds__(64 * FastCfg<OUT>::NW)
 __attribute__((amdgpu_waves_per_eu(FastCfg<OUT>::NW / 4, FastCfg<OUT>::NW / 4)))
 void decode_fast_kernel(const DecodeParams p) {
@@ -357,7 +359,7 @@ void decode_fast_kernel(const DecodeParams p) {
         R.vs = rsrc4((const _Float16 *)p.vs + wrow * NG, mrec);
         R.vz = rsrc4((const _Float16 *)p.vz + wrow * NG, mrec);
         if (OUT) {
-            const int no = p.n_out;
+            const int no = OUT == 1 ? 1 : p.n_out;
             R.ko = rsrc4(p.k_odata + bh * p.n_warm * no, nwu * (uint32_t)no * 2);
             R.vo = rsrc4(p.v_odata + bh * p.n_warm * no, nwu * (uint32_t)no * 2);
             R.ki = rsrc4(p.k_oidx + (int64_t)b * p.nblk * no, (uint32_t)(p.nblk * no * 8));
@@ -397,7 +399,7 @@ void decode_fast_kernel(const DecodeParams p) {
         }
     };
     auto issue = [&](int k, int id, unsigned char *slot) {
-        if (k == kWarm) issue_warm<BK, BV, NG, OUT, LEG>(R, slot, lane, id, p.T, p.tshift, p.n_out);
+        if (k == kWarm) issue_warm<BK, BV, NG, OUT, LEG>(R, slot, lane, id, p.T, p.tshift, OUT == 1 ? 1 : p.n_out);
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
@@ -637,7 +639,7 @@ void decode_fast_kernel(const DecodeParams p) {
             //      quantizer zeroed has scale = zero = 0 and dequantizes to 0, which skips
             //      the code lookup (taken only when some outlier channel has other meta).
             if constexpr (OUT) {
-                const int no = p.n_out;
+                const int no = OUT == 1 ? 1 : p.n_out;
                 const int *ki = (const int *)(slot + L::KI);  // low words of the int64 indices
                 bool lookup = false;
                 for (int o = 0; o < no; ++o) {
@@ -727,7 +729,7 @@ void decode_fast_kernel(const DecodeParams p) {
             bool gsel1 = false;
             uint32_t ov1[4] = {0u, 0u, 0u, 0u};
             if constexpr (OUT) {
-                if (p.n_out == 1) {
+                if (OUT == 1 || p.n_out == 1) {
                     const int c = __builtin_amdgcn_readfirstlane(min(max(*(const int *)(slot + L::VI), 0), kD - 1));
                     kk1 = c & 7;
                     gsel1 = col == (c >> 3);
@@ -792,7 +794,7 @@ void decode_fast_kernel(const DecodeParams p) {
             //      three exact MFMAs per channel add sum_t P (value - round16(code s) - z) to its
             //      accumulator, in the lanes of that chunk only
             if constexpr (OUT) {
-                const int no = p.n_out;
+                const int no = OUT == 1 ? 1 : p.n_out;
                 const int *vi = (const int *)(slot + L::VI);
                 if (no == 1) {  // the value went in above; take out the zero term accz added
                     uint32_t az[4];
@@ -1029,13 +1031,13 @@ static_assert(kWaves * (kNS * 4096 + kKmetaBytes) >= (2 * kWaves * 16 + kWaves *
 static_assert(kWavesOut * (kNSOut * 4096 + kKmetaBytes) >= (2 * kWavesOut * 16 + kWavesOut * 16 * kAccRow) * 4,
               "merge area overlaps the item counter");
 int64_t decode_fast_lds_bytes(int64_t slot, int n_out) {
-    const int nw = n_out > 0 ? kWavesOut : kWaves, ns = n_out > 0 ? kNSOut : kNS;
+    const int nw = n_out > 1 ? kWavesOut : kWaves, ns = n_out > 1 ? kNSOut : kNS;
     // Q operand, plus the natural-order query rows for the outlier corrections
     const int64_t ring = nw * (ns * slot + kKmetaBytes) + 16 + (n_out > 0 ? 2 : 1) * kQldsBytes;
     const int64_t merge = (int64_t)(2 * nw * 16 + nw * 16 * kAccRow) * 4;
     return ring > merge ? ring : merge;
 }
-int decode_fast_waves(int n_out) { return n_out > 0 ? kWavesOut : kWaves; }
+int decode_fast_waves(int n_out) { return n_out > 1 ? kWavesOut : kWaves; }
 
 bool decode_fast_legacy_shape(int D, int bits, int group_size, int meta_dtype) {
     return D == kD && (bits == 2 || bits == 4) && (group_size == 32 || group_size == 64 || group_size == 128) &&
@@ -1063,7 +1065,7 @@ bool decode_fast_eligible(const DecodeParams &p, int wk) {
     return p.slot_bytes > 0 && decode_fast_lds_bytes(p.slot_bytes, p.n_out) <= kLdsCap;
 }
 
-template <int BK, int BV, int NG, int NS, bool OUT, bool LEG>
+template <int BK, int BV, int NG, int NS, int OUT, bool LEG>
 static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
     const dim3 grid((unsigned)(p.nsplit * p.Hkv * p.B * p.nchunk));  // decoded in the kernel
     const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes, OUT ? p.n_out : 0);
@@ -1080,13 +1082,15 @@ static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
 
 template <int BK, int BV, int NG, bool LEG>
 static hipError_t launch_fast(const DecodeParams &p, hipStream_t s) {
-    return launch_fast_ns<BK, BV, NG, kNS, false, LEG>(p, s);
+    return launch_fast_ns<BK, BV, NG, kNS, 0, LEG>(p, s);
 }
 
 template <int BK, int BV, bool LEG>
 static hipError_t launch_fast_ng(const DecodeParams &p, hipStream_t s) {
     if (!LEG && p.n_out > 0)
-        return p.Gv == 32 ? launch_fast_ns<BK, BV, 4, kNSOut, true, false>(p, s) : hipErrorInvalidValue;
+        return p.Gv != 32 ? hipErrorInvalidValue
+               : p.n_out == 1 ? launch_fast_ns<BK, BV, 4, kNS, 1, false>(p, s)
+                              : launch_fast_ns<BK, BV, 4, kNSOut, kMaxOut, false>(p, s);
     if (p.Gv == 32) return launch_fast<BK, BV, 4, LEG>(p, s);
     if (p.Gv == 64) return launch_fast<BK, BV, 2, LEG>(p, s);
     if (p.Gv == 128) return launch_fast<BK, BV, 1, LEG>(p, s);

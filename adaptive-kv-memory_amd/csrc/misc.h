@@ -41,6 +41,7 @@ struct ImportanceParams {
 };
 
 hipError_t dequant_launch(const DequantParams &p, hipStream_t s);
+hipError_t stream_read_launch(const void *p, int64_t bytes, uint32_t *sink, hipStream_t s);
 hipError_t bitpack_launch(const void *codes, void *packed, int64_t rows, int dim, int bits, int prow, hipStream_t s);
 hipError_t bitunpack_launch(const void *packed, void *codes, int64_t rows, int prow, int dim, int bits, hipStream_t s);
 hipError_t importance_launch(const ImportanceParams &p, hipStream_t s);

@@ -429,6 +429,23 @@ hipError_t zero_fill_launch(void *p, int64_t bytes, hipStream_t s) {
     hipLaunchKernelGGL(zero_fill_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, s, (u4 *)p, n16);
     return hipGetLastError();
 }
+// Streaming read of `bytes` (a multiple of 16) in 16-byte non-temporal loads over a
+// grid-stride loop, the loads XORed into a value that is stored only if it equals a
+// sentinel: the bandwidth a read-once kernel of that size reaches on this GPU.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u4 *__restrict__ x, int64_t n16, uint32_t *sink) {
+    u4 acc = {0u, 0u, 0u, 0u};
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        acc ^= __builtin_nontemporal_load(x + i);
+    const uint32_t r = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+    if (r == 0x5A17C0DEu) sink[0] = r;
+}
+hipError_t stream_read_launch(const void *p, int64_t bytes, uint32_t *sink, hipStream_t s) {
+    const int64_t n16 = bytes / 16;
+    if (n16 <= 0) return hipSuccess;
+    // 2048 workgroups of 256 threads: the fastest of 1024-8192 for 73 MB - 1 GB reads
+    hipLaunchKernelGGL(stream_read_kernel, dim3(2048), dim3(256), 0, s, (const u4 *)p, n16, sink);
+    return hipGetLastError();
+}
 hipError_t importance_launch(const ImportanceParams &p, hipStream_t s) {
     if (p.n_scores == 0) return hipSuccess;
     hipLaunchKernelGGL(importance_kernel, dim3((unsigned)((p.n_scores + 255) / 256)), dim3(256), 0, s, p);

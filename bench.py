@@ -226,11 +226,14 @@ def main():
                      "algorithmic_bytes_per_launch": alg,
                      "us_per_launch": round(us_layer_attn, 3)},
     }
+    del g_full, g_attn, full, attn_only
+    torch.cuda.empty_cache()
+    add_stream_reference(res["roofline"])
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline", file=sys.stderr, flush=True)
         res["cpu_baseline"] = cpu_baseline(layers[0], s)
     if not args.no_other_workloads and L == s.layers:
-        del g_full, g_attn, full, attn_only, layers
+        del layers
         torch.cuda.empty_cache()
         res["workloads"] = other_workloads(args)
     if args.calib_copy:
@@ -239,6 +242,50 @@ def main():
         torch.neg(src, out=dst)  # one elementwise kernel: reads and writes CALIB_BYTES
         torch.cuda.synchronize()
     print(json.dumps(res), flush=True)
+
+
+def stream_read_reference(nbytes, launches=28, steps=10):
+    """The same byte count read once by akv_stream_read (16-byte non-temporal loads over
+    a grid-stride loop, nothing else): what a read-once kernel of that size reaches on
+    this GPU, launch included.  Successive launches read different regions of a buffer
+    of at least 1 GiB, so the 256 MB Infinity Cache does not serve them; sizes above
+    1 GiB are timed at 1 GiB and scaled."""
+    import ctypes
+    import torch
+    from akv import _native as nat
+    lib = nat.load()
+    n = min(int(nbytes) // 16 * 16, 1 << 30)
+    regions = max(1, (1 << 30) // n)
+    buf = torch.ones((regions * n) // 2, dtype=torch.float16, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+    def launch(k):  # on the current stream (the capture stream inside the graph)
+        stream = torch.cuda.current_stream().cuda_stream
+        nat.check(lib.akv_stream_read(ctypes.c_void_p(buf.data_ptr() + (k % regions) * n), n,
+                                      ctypes.c_void_p(sink.data_ptr()), ctypes.c_void_p(stream)), "stream read")
+    launch(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for k in range(launches):
+            launch(k)
+    ms, _ = _event_time(g.replay, steps, 2)
+    us = ms * 1e3 / launches
+    gbps = n / (us * 1e-6) / 1e9
+    del g, buf
+    torch.cuda.empty_cache()
+    return {"GBps": round(gbps, 1), "us_per_launch": round(nbytes / (gbps * 1e9) * 1e6, 3),
+            "bytes_timed": n, "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
+def add_stream_reference(roof):
+    """Put the streaming-read figure for the roofline's algorithmic bytes beside it."""
+    try:
+        ref = stream_read_reference(roof["algorithmic_bytes_per_launch"])
+        ref["kernel_frac_of_stream"] = round(roof["achieved"] / ref["GBps"], 4)
+        roof["stream_read"] = ref
+    except Exception as e:  # the reference figure is informative only
+        roof["stream_read"] = {"error": f"{type(e).__name__}: {e}"}
 
 
 SUMMARY_KEYS = ("metric", "value", "unit", "ms_per_call", "us_per_layer", "ms_quantize_only", "roofline",
@@ -305,6 +352,7 @@ def bench_c1(args):
                         "kernel": "akv_decode_attn, 32 launches per graph replay (1.7 MB per layer: launch-bound, "
                                   "and the layer stays in the 256 MB Infinity Cache)",
                         "algorithmic_bytes_per_launch": nb["attn_total"]}}
+    add_stream_reference(res["roofline"])
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
         host = {n: getattr(warm, n).cpu().numpy() for n in ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
@@ -406,6 +454,7 @@ def bench_production(args):
            "reference_design_gpu": {"us_per_layer": round(ref_ms * 1e3 / L, 3),
                                     "bytes_per_layer": ref_bytes,
                                     "what": "cached fp16 warm copy + hot copy, torch matmul/softmax/matmul"}}
+    add_stream_reference(res["roofline"])
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
         lay = cache._layers[0]
@@ -497,6 +546,7 @@ def bench_kivi(args):
            "reference_design_gpu": {"us_per_layer": round(ref_ms * 1e3 / L, 3),
                                     "what": "float16 working copy + residual concatenated, torch "
                                             "matmul/softmax/matmul"}}
+    add_stream_reference(res["roofline"])
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
         t_k, t_v = cache._quant_keys[0], cache._quant_values[0]
@@ -696,6 +746,7 @@ def bench_decode_mha(args):
                         "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": recorded_traffic(s.name),
                         "kernel": "akv_decode_attn per layer (decode_fast_kernel with outlier channels)",
                         "algorithmic_bytes_per_launch": alg, "us_per_launch": round(us_layer, 3)}}
+    add_stream_reference(res["roofline"])
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(layers[0], s, budget_s=10.0)
     return res

@@ -322,6 +322,12 @@ const char *akv_last_error(void);
  * 0 akv_warm_desc, 1 akv_decode_args, 2 akv_quant_args, 3 akv_dequant_args,
  * 4 akv_importance_args, 5 akv_prefill_args; -1 for an unknown id. */
 int64_t akv_struct_size(int32_t which);
+/* A measurement helper with no counterpart in the reference: reads `bytes` (a multiple of
+ * 16, 16-byte aligned) once with 16-byte non-temporal loads, as fast as a read-once kernel
+ * goes on this GPU; `sink` (4 bytes of device memory) is written only if the XOR of the data
+ * equals a sentinel.  Its time beside a kernel's, over the same byte count, is the streaming
+ * roofline the benchmark reports. */
+int akv_stream_read(const void *data, int64_t bytes, uint32_t *sink, void *stream);
 
 #ifdef __cplusplus
 }

@@ -57,6 +57,10 @@ def test_host_side_validation_without_gpu():
         nat.check(nat.AKV_E_BITS, "x")
     assert lib.akv_bitpack(None, None, 1, 8, 7, None) == nat.AKV_E_BITS
     assert lib.akv_bitunpack(None, None, 1, 2, 9, 2, None) == nat.AKV_E_SHAPE
+    assert lib.akv_stream_read(None, 24, None, None) == nat.AKV_E_SHAPE  # not a multiple of 16
+    assert lib.akv_stream_read(None, 32, None, None) == nat.AKV_E_INVALID
+    assert lib.akv_stream_read(ctypes.c_void_p(8), 32, ctypes.c_void_p(16), None) == nat.AKV_E_ALIGN
+    assert lib.akv_stream_read(None, 0, None, None) == nat.AKV_OK
 
 
 def test_decode_shape_checks():
