@@ -437,7 +437,12 @@ void decode_fast_kernel(const DecodeParams p) {
     for (int s2 = 1; s2 < NS; ++s2) qk[s2] = kNone;
     bool primed = false;
     __syncthreads();  // Q operand and item counter in LDS before any wave uses them
-    auto qop = [&](int st) { return __builtin_bit_cast(h8, qlds[st * 64 + lane]); };
+    // the query operand stays in registers for the whole range (16 VGPRs): one LDS read per
+    // MFMA step less in every unit
+    h8 qreg[KSTEPS];
+#pragma unroll
+    for (int st = 0; st < KSTEPS; ++st) qreg[st] = __builtin_bit_cast(h8, qlds[st * 64 + lane]);
+    auto qop = [&](int st) { return qreg[st]; };
 
     Soft stt;
     stt.m2 = -INFINITY;
@@ -519,13 +524,46 @@ void decode_fast_kernel(const DecodeParams p) {
             __builtin_amdgcn_wave_barrier();
         }
         {
+            // ---- LDS reads at the top of the unit, issued together (the empty asm with a memory
+            //      clobber keeps them above it, so their latencies overlap instead of each read
+            //      being waited for before the next is issued): the lane's packed K rows of both
+            //      halves, the V scales of the overflow test, and (block-affine) the lane's K-meta
+            //      pair of the prep below
+            uint32_t kraw[2][BK];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t *kp = (const uint32_t *)(slot + k_lane + 16 * h * L::KR);
+#pragma unroll
+                for (int jj = 0; jj < BK; ++jj) kraw[h][jj] = kp[jj];
+            }
+            h2 vsv = {};
+            if (!LEG && lane * 4 < L::VMB) vsv = as_h2(*(const uint32_t *)(slot + L::VS + 4 * lane));
+            h2 s2v = {}, z2v = {};
+            if constexpr (!LEG) {
+                s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
+                z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
+            }
+            asm volatile("" ::: "memory");
+            KWin<BK> W[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) k_windows<BK>(kraw[h], W[h]);
+            // ---- the V fast path holds when no -1024 s of the unit's V scales overflows
+            bool vfast;
+            {
+                bool vfin = true;
+                if (!LEG && lane * 4 < L::VMB) {
+                    const _Float16 n0 = (_Float16)(-1024.0f);
+                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
+                }
+                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
+            }
             // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS
             //      and read back per MFMA step; the fast paths hold when no -1024 s overflows
             //      (K and V scales of the unit).  LEG: the lane's 32 channels lie in one group,
             //      so its token has one (s, z) per half, read from the slot; the value is
             //      round16(c s + z) in one fma (the reference dequantizes this layout in fp32 and
             //      rounds once), and the symmetric branch round16((c - half_max) s).
-            bool kfast = true, vfast;
+            bool kfast = true;
             h2 ls[2] = {}, lz[2] = {};
             if constexpr (LEG) {
 #pragma unroll
@@ -537,8 +575,6 @@ void decode_fast_kernel(const DecodeParams p) {
                     lz[h] = (h2){zv, zv};
                 }
             } else {
-                const h2 s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
-                const h2 z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
                 const h2 n2 = s2v * (h2){nmul, nmul};
                 const uint32_t nb = as_u32(n2);
                 kfast = !__builtin_amdgcn_ballot_w64(!finite2(nb));
@@ -548,28 +584,10 @@ void decode_fast_kernel(const DecodeParams p) {
                 kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
                 __builtin_amdgcn_wave_barrier();
             }
-            {
-                bool vfin = true;
-                if (!LEG && lane * 4 < L::VMB) {
-                    const h2 vsv = as_h2(*(const uint32_t *)(slot + L::VS + 4 * lane));
-                    const _Float16 n0 = (_Float16)(-1024.0f);
-                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
-                }
-                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
-            }
             const u4 *kmr = (const u4 *)kmeta;
 
             const int tok0 = id * kUnit;  // first token of the unit (pair-local warm index)
             // ---- QK of both 16-token halves, step by step (two independent MFMA chains)
-            KWin<BK> W[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                uint32_t kraw[BK];
-                const uint32_t *kp = (const uint32_t *)(slot + k_lane + 16 * h * L::KR);
-#pragma unroll
-                for (int jj = 0; jj < BK; ++jj) kraw[jj] = kp[jj];
-                k_windows<BK>(kraw, W[h]);
-            }
             f4 sc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
             if constexpr (LEG) {
 #pragma unroll
@@ -676,6 +694,36 @@ void decode_fast_kernel(const DecodeParams p) {
                 }
             }
 
+            // ---- V: lane (chunk col, tokens 4 grp .. +3 of each half); token pairs per dword
+            //      (read here, before the softmax, so the LDS reads are in flight while it runs;
+            //      the code reads share one base address and take immediate offsets)
+            uint32_t vraw[2][4];
+            {
+                const lds_cu32 *vq = lds_ptr<uint32_t>(in_vgpr(lds_addr(slot) + (uint32_t)(v_lane & ~3)));
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+                        const int o = (16 * h + ii) * L::VR / 4;
+                        if (BV == 3) {  // the chunk's 3 bytes from the aligned 8 around them
+                            vraw[h][ii] = __builtin_amdgcn_alignbyte(vq[o + 1], vq[o], v_lane & 3);
+                        } else if (BV == 2) {
+                            vraw[h][ii] = lds_u16(slot + v_lane + (16 * h + ii) * L::VR);
+                        } else {
+                            vraw[h][ii] = vq[o];
+                        }
+                    }
+            }
+            h2 vs[2][2], vz[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int pp = 0; pp < 2; ++pp) {
+                    const int ta = 16 * h + 2 * pp;  // + 4 grp (in vm_lane)
+                    vs[h][pp] = lds_h2(slot + L::VS + vm_lane + ta * NG * 2, slot + L::VS + vm_lane + (ta + 1) * NG * 2);
+                    vz[h][pp] = lds_h2(slot + L::VZ + vm_lane + ta * NG * 2, slot + L::VZ + vm_lane + (ta + 1) * NG * 2);
+                    if (LEG && symv) vz[h][pp] = (h2){(_Float16)0, (_Float16)0};  // symmetric: no zero-point
+                }
             // ---- softmax over the 32 tokens (ragged tail masked; logits stashed)
             if (tok0 + kUnit > nw) {
 #pragma unroll
@@ -695,28 +743,6 @@ void decode_fast_kernel(const DecodeParams p) {
             }
             const h8 pop = softmax32(stt, sc[0], sc[1], sl2);
 
-            // ---- V: lane (chunk col, tokens 4 grp .. +3 of each half); token pairs per dword
-            uint32_t vraw[2][4];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    const unsigned char *vp = slot + v_lane + (16 * h + ii) * L::VR;
-                    if (BV == 3) {  // the chunk's 3 bytes from the aligned 8 around them
-                        const uint32_t *vq = (const uint32_t *)(slot + (v_lane & ~3) + (16 * h + ii) * L::VR);
-                        vraw[h][ii] = __builtin_amdgcn_alignbyte(vq[1], vq[0], v_lane & 3);
-                    } else vraw[h][ii] = BV == 2 ? lds_u16(vp) : *(const uint32_t *)vp;
-                }
-            h2 vs[2][2], vz[2][2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-#pragma unroll
-                for (int pp = 0; pp < 2; ++pp) {
-                    const int ta = 16 * h + 2 * pp;  // + 4 grp (in vm_lane)
-                    vs[h][pp] = lds_h2(slot + L::VS + vm_lane + ta * NG * 2, slot + L::VS + vm_lane + (ta + 1) * NG * 2);
-                    vz[h][pp] = lds_h2(slot + L::VZ + vm_lane + ta * NG * 2, slot + L::VZ + vm_lane + (ta + 1) * NG * 2);
-                    if (LEG && symv) vz[h][pp] = (h2){(_Float16)0, (_Float16)0};  // symmetric: no zero-point
-                }
             uint32_t win[2][2][VSlot<BV>::NW];
 #pragma unroll
             for (int h = 0; h < 2; ++h)

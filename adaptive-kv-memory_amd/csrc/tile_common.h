@@ -111,6 +111,14 @@ __device__ __forceinline__ uint32_t in_vgpr(uint32_t x) {
     return x;
 }
 
+// An LDS pointer made from a 32-bit LDS byte address (for example one kept opaque by
+// in_vgpr, so that the constant parts of later addresses become instruction offsets).
+typedef const __attribute__((address_space(3))) uint32_t lds_cu32;
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(3))) T *lds_ptr(uint32_t a) {
+    return (const __attribute__((address_space(3))) T *)(size_t)a;
+}
+
 __device__ __forceinline__ h2 pk_fma(h2 a, h2 b, h2 c) { return __builtin_elementwise_fma(a, b, c); }
 
 __device__ __forceinline__ float wmax16(float x) {
