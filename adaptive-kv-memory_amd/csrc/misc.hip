@@ -156,6 +156,47 @@ __global__ __launch_bounds__(kImpTile) void importance_kernel(const ImportancePa
     p.scores[n] = s;
 }
 
+// Without key pooling: a workgroup owns 64 keys and its RG waves split the (batch x
+// head) rows into RG contiguous ranges (every query row m >= m0 of them), 8 loads in
+// flight per lane; the RG partial sums are added in range order.  The row loads of a
+// wave cover 64 consecutive keys (256 coalesced bytes at fp32).  Sum order: over the
+// rows of a range, then over the ranges, then divided by B*H -- the same sum as
+// key_importance in another association (fp32 rounding differs in the last bits).
+// RG = 16 when there are too few key tiles to fill the GPU with RG = 4.
+constexpr int kImpKeys = 64;
+template <int RG>
+__global__ __launch_bounds__(64 * RG) void importance_rows_kernel(const ImportanceParams p) {
+    __shared__ float part[RG][kImpKeys];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t n = (int64_t)blockIdx.x * kImpKeys + lane;
+    const int64_t bhn = p.B * p.H, per = (bhn + RG - 1) / RG;
+    const int64_t bh0 = min(bhn, per * w), bh1 = min(bhn, bh0 + per);
+    float acc = 0.f;
+    if (n < p.N) {
+        for (int64_t m = p.m0; m < p.M; ++m) {
+            int64_t bh = bh0;
+            for (; bh + 8 <= bh1; bh += 8) {
+                float x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = load_as_f32(p.attn, ((bh + j) * p.M + m) * p.N + n, p.attn_dt);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc += x[j];
+            }
+            for (; bh < bh1; ++bh) acc += load_as_f32(p.attn, (bh * p.M + m) * p.N + n, p.attn_dt);
+        }
+    }
+    part[w][lane] = acc;
+    __syncthreads();
+    if (w != 0 || n >= p.n_scores) return;
+    float tot = 0.f;
+#pragma unroll
+    for (int r = 0; r < RG; ++r) tot += part[r][lane];
+    const float imp = n < p.N ? tot / (float)bhn : 0.f;
+    float sc = p.scores[n] * p.decay;
+    sc = sc + imp;
+    p.scores[n] = sc;
+}
+
 // ------------------------------------------------------------ demote selection
 // One workgroup (1024 threads) per row.  Scores become order-preserving 32-bit
 // keys (-0 as +0, NaN above +inf, protected positions = +inf); a 4-pass radix
@@ -448,7 +489,14 @@ hipError_t stream_read_launch(const void *p, int64_t bytes, uint32_t *sink, hipS
 }
 hipError_t importance_launch(const ImportanceParams &p, hipStream_t s) {
     if (p.n_scores == 0) return hipSuccess;
-    hipLaunchKernelGGL(importance_kernel, dim3((unsigned)((p.n_scores + 255) / 256)), dim3(256), 0, s, p);
+    if (p.pool <= 1) {
+        const unsigned tiles = (unsigned)((p.n_scores + kImpKeys - 1) / kImpKeys);
+        const int64_t rows = p.B * p.H * (p.M - p.m0);
+        if (tiles >= 512 || rows < 64) hipLaunchKernelGGL(importance_rows_kernel<4>, dim3(tiles), dim3(256), 0, s, p);
+        else hipLaunchKernelGGL(importance_rows_kernel<16>, dim3(tiles), dim3(1024), 0, s, p);
+    } else {
+        hipLaunchKernelGGL(importance_kernel, dim3((unsigned)((p.n_scores + 255) / 256)), dim3(256), 0, s, p);
+    }
     return hipGetLastError();
 }
 
