@@ -671,8 +671,10 @@ void decode_fast_kernel(const DecodeParams p) {
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         const h4 od = *(const h4 *)(slot + L::KO + 2 * (16 * h + 4 * grp));  // tokens 4 grp .. +3
+                        // q[c] * value is exact in fp32 (two fp16 factors), so one fma equals the
+                        // product-then-add and takes the fp16 operands directly (v_fma_mix)
 #pragma unroll
-                        for (int i = 0; i < 4; ++i) sc[h][i] += qd * (float)od[i];
+                        for (int i = 0; i < 4; ++i) sc[h][i] = __builtin_fmaf(qd, (float)od[i], sc[h][i]);
                     }
                 } else {
                     for (int o = 0; o < no; ++o) {
