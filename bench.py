@@ -68,40 +68,45 @@ def layer_bytes(s):
 
 
 def cpu_baseline(layer0, s, budget_s=12.0):
-    """Oracle restatement of the reference CPU path on layer 0, batch elements
+    """The reference CPU path restated with torch CPU ops (fp16 dequant, head expansion
+    and concatenation, fp32 attention, importance update) on layer 0, batch elements
     taken one at a time until ~budget_s seconds of CPU work."""
-    import numpy as np
-    from threadpoolctl import threadpool_limits
-    from oracle import affine as oaff
-    from oracle import attention as oatt
-    from oracle import importance as oimp
+    import torch
+    from oracle import torch_cpu as otc
     cores = len(os.sched_getaffinity(0))
     q, kh, vh, warm, _ = layer0
     names = ["k_codes", "k_scale", "k_zero", "v_codes", "v_scale", "v_zero"]
     n_out = 0 if warm.k_oidx is None else warm.k_oidx.shape[-1]
     if n_out:
         names += ["k_oidx", "v_oidx", "k_odata", "v_odata"]
-    host = {k: getattr(warm, k).cpu().numpy() for k in names}
-    qn, khn, vhn = q.cpu().numpy(), kh.cpu().numpy(), vh.cpu().numpy()
+    host = {k: getattr(warm, k).cpu() for k in names}
+    for k in ("k_oidx", "v_oidx"):
+        if k in host:
+            host[k] = host[k].long()
+    qc, khc, vhc = q.cpu(), kh.cpu(), vh.cpu()
     done, t_cpu = 0, 0.0
-    scores = np.zeros(s.N, np.float32)
-    with threadpool_limits(limits=cores):
+    scores = torch.zeros(s.N, dtype=torch.float32)
+    threads = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
         while done < s.B and t_cpu < budget_s:
             b = done
             w = {k: v[b:b + 1] for k, v in host.items()}
             w.update(bits_k=s.bits_k, bits_v=s.bits_v, T=s.block_t, G=s.group_v, D=s.D, N=s.n_warm, n_out=n_out)
             t0 = time.perf_counter()
-            kd, vd = oaff.dequant_kv_blocked(w)
-            _, attn = oatt.mixed_attention_fp32(qn[b:b + 1], khn[b:b + 1], vhn[b:b + 1], kd, vd, hot_first=False,
-                                                return_weights=s.decay is not None)
+            kd, vd = otc.dequant_kv_blocked(w)
+            _, attn = otc.decode_attention(qc[b:b + 1], khc[b:b + 1], vhc[b:b + 1], kd, vd, hot_first=False,
+                                           return_weights=s.decay is not None)
             if s.decay is not None:
-                scores = oimp.fused_importance_update(attn, scores, s.decay)
+                scores = otc.importance_update(attn, scores, s.decay)
             t_cpu += time.perf_counter() - t0
             done += 1
+    finally:
+        torch.set_num_threads(threads)
     kv_bytes = layer_bytes(s)["kv"] * done / s.B
     return {"value": round(kv_bytes / t_cpu / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"layer 0, {done} of {s.B} sequences (dequant + fp32 attention"
-                      f"{' + importance' if s.decay is not None else ''}), "
+            "sample": f"layer 0, {done} of {s.B} sequences (torch CPU: fp16 dequant, repeat_kv + cat, fp32 "
+                      f"attention{' + importance' if s.decay is not None else ''}), "
                       f"{t_cpu:.1f} s on {cores} host threads",
             "us_per_layer_equiv": round(t_cpu / done * s.B * 1e6, 1)}
 
@@ -313,17 +318,15 @@ def other_workloads(args):
 
 def bench_c1(args):
     """Qwen2.5-1.5B shape at 4k context (B1, 12/2 heads, 512 hot + 3584 warm 4/4-bit, two K
-    channels per kv head x10): the reference's CPU path -- the oracle restatement of the
-    fp32 dequant-attention (akv/triton_kernels.py:350-387) timed on the host cores -- and
-    the same layer on the GPU (one akv_decode_attn launch)."""
-    import numpy as np
+    channels per kv head x10): the reference's CPU path -- its fp16 dequant and fp32
+    attention (akv/affine_quantizer.py:112-124, akv/triton_kernels.py:350-387) restated
+    with torch CPU ops and timed on the host cores -- and the same layer on the GPU (one
+    akv_decode_attn launch)."""
     import torch
     import akv
     from akv import workloads as wl
     from akv.warm_tier import DecodeCall
-    from threadpoolctl import threadpool_limits
-    from oracle import affine as oaff
-    from oracle import attention as oatt
+    from oracle import torch_cpu as otc
     s = wl.QWEN_DECODE_4K
     k, v = wl.make_kv(s, device="cuda")
     q = wl.make_q(s, device="cuda")
@@ -355,21 +358,25 @@ def bench_c1(args):
     add_stream_reference(res["roofline"])
     if not args.no_cpu_baseline:
         cores = len(os.sched_getaffinity(0))
-        host = {n: getattr(warm, n).cpu().numpy() for n in ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
-                                                             "v_zero")}
+        host = {n: getattr(warm, n).cpu() for n in ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale", "v_zero")}
         host.update(bits_k=s.bits_k, bits_v=s.bits_v, T=s.block_t, G=s.group_v, D=s.D, N=s.n_warm, n_out=0)
-        qn, khn, vhn = q.cpu().numpy(), kh.cpu().numpy(), vh.cpu().numpy()
+        qc, khc, vhc = q.cpu(), kh.cpu(), vh.cpu()
         reps, t_cpu = 0, 0.0
-        with threadpool_limits(limits=cores):
+        threads = torch.get_num_threads()
+        torch.set_num_threads(cores)
+        try:
             while t_cpu < 3.0 or reps < 3:
                 t0 = time.perf_counter()
-                kd, vd = oaff.dequant_kv_blocked(host)
-                oatt.mixed_attention_fp32(qn, khn, vhn, kd, vd, hot_first=False, return_weights=False)
+                kd, vd = otc.dequant_kv_blocked(host)
+                otc.decode_attention(qc, khc, vhc, kd, vd, hot_first=False, return_weights=False)
                 t_cpu += time.perf_counter() - t0
                 reps += 1
+        finally:
+            torch.set_num_threads(threads)
         us = t_cpu / reps * 1e6
         res["cpu_baseline"] = {"value": round(us, 1), "unit": "us per layer", "cores": cores, "kind": "port",
-                               "sample": f"the whole layer (dequant + fp32 attention), {reps} runs, "
+                               "sample": f"the whole layer (torch CPU: fp16 dequant, repeat_kv + cat, fp32 "
+                                         f"attention), {reps} runs, "
                                          f"{t_cpu:.1f} s on {cores} host threads",
                                "kv_gbps": round(nb["kv"] / (us * 1e-6) / 1e9, 4)}
     return res
@@ -759,9 +766,7 @@ def bench_prefill(args):
     import torch
     import akv
     from akv import workloads as wl
-    from threadpoolctl import threadpool_limits
-    from oracle import affine as oaff
-    from oracle import attention as oatt
+    from oracle import torch_cpu as otc
     s = wl.LLAMA70B_PREFILL_128K
     print(f"[bench] building {s.name}", file=sys.stderr, flush=True)
     k, v = wl.make_kv(s, device="cuda")
@@ -784,23 +789,28 @@ def bench_prefill(args):
                         "frac": round(tflops / 2500.0, 4), "traffic": recorded_traffic(s.name),
                         "kernel": "prefill_kernel (one launch at this shape)", "flops_per_launch": flops}}
     if not args.no_cpu_baseline:
-        # oracle: dequant + fp32 attention of kv-head 0's 8 query heads at 16 positions
-        host = {n: getattr(warm, n)[:, :1].cpu().numpy() for n in ("k_codes", "k_scale", "k_zero",
-                                                                    "v_codes", "v_scale", "v_zero")}
+        # torch CPU restatement: dequant + fp32 attention of kv-head 0's 8 query heads at 16 positions
+        host = {n: getattr(warm, n)[:, :1].cpu() for n in ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
+                                                           "v_zero")}
         host.update(bits_k=s.bits_k, bits_v=s.bits_v, T=s.block_t, G=s.group_v, D=s.D, N=s.n_warm, n_out=0)
         g = s.Hq // s.Hkv
-        qs = q[:, :g, :16].float().cpu().numpy()
-        khn, vhn = kh[:, :1].cpu().numpy(), vh[:, :1].cpu().numpy()
+        qs = q[:, :g, :16].cpu()
+        khc, vhc = kh[:, :1].cpu(), vh[:, :1].cpu()
         cores = len(os.sched_getaffinity(0))
-        with threadpool_limits(limits=cores):
+        threads = torch.get_num_threads()
+        torch.set_num_threads(cores)
+        try:
             t0 = time.perf_counter()
-            kd, vd = oaff.dequant_kv_blocked(host)
-            oatt.mixed_attention_fp32(qs, khn, vhn, kd, vd, return_weights=False)
+            kd, vd = otc.dequant_kv_blocked(host)
+            otc.decode_attention(qs, khc, vhc, kd, vd, hot_first=True, return_weights=False)
             t_cpu = time.perf_counter() - t0
+        finally:
+            torch.set_num_threads(threads)
         f_cpu = 4.0 * g * 16 * s.N * s.D
         res["cpu_baseline"] = {"value": round(f_cpu / t_cpu / 1e12, 6), "unit": "TFLOP/s", "cores": cores,
-                               "kind": "port", "sample": f"kv-head 0, 8 query heads x 16 positions: dequant + fp32 "
-                                                         f"attention over 131072 tokens, {t_cpu:.1f} s"}
+                               "kind": "port", "sample": f"kv-head 0, 8 query heads x 16 positions, torch CPU: fp16 "
+                                                         f"dequant + fp32 attention over 131072 tokens, "
+                                                         f"{t_cpu:.1f} s on {cores} host threads"}
     return res
 
 
