@@ -67,10 +67,10 @@ def layer_bytes(s):
             "kv": hot + codes + kmeta + vmeta, "attn_total": q + hot + codes + kmeta + vmeta + out}
 
 
-def cpu_baseline(layer0, s, budget_s=12.0):
+def cpu_baseline(layer0, s, budget_s=12.0, min_s=5.0):
     """The reference CPU path restated with torch CPU ops (fp16 dequant, head expansion
     and concatenation, fp32 attention, importance update) on layer 0, batch elements
-    taken one at a time until ~budget_s seconds of CPU work."""
+    taken one at a time (cycling) for min_s to budget_s seconds of CPU work."""
     import torch
     from oracle import torch_cpu as otc
     cores = len(os.sched_getaffinity(0))
@@ -89,8 +89,9 @@ def cpu_baseline(layer0, s, budget_s=12.0):
     threads = torch.get_num_threads()
     torch.set_num_threads(cores)
     try:
-        while done < s.B and t_cpu < budget_s:
-            b = done
+        # every sequence of the layer at least once, cycling until min_s of work, at most budget_s
+        while (done < s.B or t_cpu < min_s) and t_cpu < budget_s:
+            b = done % s.B
             w = {k: v[b:b + 1] for k, v in host.items()}
             w.update(bits_k=s.bits_k, bits_v=s.bits_v, T=s.block_t, G=s.group_v, D=s.D, N=s.n_warm, n_out=n_out)
             t0 = time.perf_counter()
@@ -105,7 +106,8 @@ def cpu_baseline(layer0, s, budget_s=12.0):
         torch.set_num_threads(threads)
     kv_bytes = layer_bytes(s)["kv"] * done / s.B
     return {"value": round(kv_bytes / t_cpu / 1e9, 4), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"layer 0, {done} of {s.B} sequences (torch CPU: fp16 dequant, repeat_kv + cat, fp32 "
+            "sample": f"layer 0, {done} sequence passes over its {s.B} sequences (torch CPU: fp16 dequant, "
+                      f"repeat_kv + cat, fp32 "
                       f"attention{' + importance' if s.decay is not None else ''}), "
                       f"{t_cpu:.1f} s on {cores} host threads",
             "us_per_layer_equiv": round(t_cpu / done * s.B * 1e6, 1)}
