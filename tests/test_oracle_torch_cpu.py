@@ -46,3 +46,28 @@ def test_decode_path_matches_oracle(bk, bv, n_out_frac):
     exp = oimp.fused_importance_update(attn, sc, 0.9)
     got = otc.importance_update(tattn, torch.from_numpy(sc), 0.9).numpy()
     np.testing.assert_allclose(got, exp, rtol=1e-5, atol=1e-8)
+
+
+@pytest.mark.parametrize("of", [0.0, 0.02])
+def test_bench_cpu_baseline_runs_on_host_tensors(of):
+    """The bench's CPU-baseline leg on a small layer held in host tensors: it runs every
+    sequence at least once and reports the fields of the bench line."""
+    import bench
+    import akv
+    from akv import workloads as wl
+    rng = np.random.default_rng(3)
+    s = wl.DecodeShape("t", 2, 6, 2, 128, 32, 256, 3, 3, decay=0.9)
+    k = rng.standard_normal((s.B, s.Hkv, s.n_warm, s.D)).astype(np.float16)
+    v = rng.standard_normal((s.B, s.Hkv, s.n_warm, s.D)).astype(np.float16)
+    w = oaff.quantize_kv_blocked(k, v, 3, 3, 32, 32, outlier_fraction=of)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x))
+    n_out = w.get("n_out", 0)
+    warm = akv.WarmTier(t(w["k_codes"]), t(w["k_scale"]), t(w["k_zero"]), t(w["v_codes"]), t(w["v_scale"]),
+                        t(w["v_zero"]), 3, 3, 32, 32, 128,
+                        *( [t(w["k_oidx"]), t(w["v_oidx"]), t(w["k_odata"]), t(w["v_odata"])] if n_out else []))
+    q = torch.randn(s.B, s.Hq, 1, s.D).half()
+    kh = torch.randn(s.B, s.Hkv, s.n_hot, s.D).half()
+    vh = torch.randn(s.B, s.Hkv, s.n_hot, s.D).half()
+    res = bench.cpu_baseline((q, kh, vh, warm, None), s, budget_s=2.0, min_s=0.2)
+    assert res["kind"] == "port" and res["unit"] == "GB/s" and res["value"] > 0
+    assert res["cores"] >= 1 and "importance" in res["sample"]
