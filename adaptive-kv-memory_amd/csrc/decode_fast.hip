@@ -61,6 +61,8 @@
 // A block whose scales would overflow -2^(10-o) s in fp16 (|s| >= 64) takes
 // a slower exact path: the code is recovered as an fp16 integer, then
 // round16(c * s) and round16(. + z) are two packed ops.
+#include <atomic>
+
 #include "akv_common.h"
 #include "decode.h"
 #include "tile_common.h"
@@ -1097,12 +1099,18 @@ template <int BK, int BV, int NG, int NS, int OUT, bool LEG>
 static hipError_t launch_fast_ns(const DecodeParams &p, hipStream_t s) {
     const dim3 grid((unsigned)(p.nsplit * p.Hkv * p.B * p.nchunk));  // decoded in the kernel
     const size_t lds = (size_t)decode_fast_lds_bytes(p.slot_bytes, OUT ? p.n_out : 0);
-    static bool attr_set = false;  // raise the dynamic LDS cap above 64 KiB once
-    if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS, OUT, LEG>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCap);
+    // raise the dynamic LDS cap above 64 KiB once per device (a bit per device index;
+    // host threads that race here both set it, which is harmless)
+    static std::atomic<uint64_t> attr_devs{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
+    if (!bit || !(attr_devs.load(std::memory_order_acquire) & bit)) {
+        e = hipFuncSetAttribute((const void *)decode_fast_kernel<BK, BV, NG, NS, OUT, LEG>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kLdsCap);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        attr_devs.fetch_or(bit, std::memory_order_release);
     }
     hipLaunchKernelGGL((decode_fast_kernel<BK, BV, NG, NS, OUT, LEG>), grid, dim3(64 * FastCfg<OUT>::NW), lds, s, p);
     return hipGetLastError();
