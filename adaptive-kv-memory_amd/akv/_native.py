@@ -245,5 +245,31 @@ def workspace(nbytes: int, device, zero_prefix: int = 0) -> torch.Tensor:
     return ws
 
 
+class DecodeWorkspace:
+    """A decode workspace reused across calls on one device and stream.
+
+    A call needs its first ``counter_bytes`` bytes (the split arrival counters) at
+    zero and leaves exactly those bytes at zero when it completes; the bytes after
+    them hold its split partials.  So after a call only the prefix that call used is
+    known to be zero: a later call with a smaller counter region writes partials over
+    the tail of the larger one, and a call after that with the larger region must
+    zero it again.  ``get`` keeps the last call's counter size (not the largest ever
+    zeroed) and clears the prefix whenever a call needs more of it.  Calls that share
+    one workspace must be ordered on one stream."""
+
+    def __init__(self):
+        self._buf: Optional[torch.Tensor] = None
+        self._zero = 0  # bytes at the start known to be zero when the next call starts
+
+    def get(self, nbytes: int, counter_bytes: int, device) -> torch.Tensor:
+        buf = self._buf
+        if buf is None or buf.numel() < nbytes or buf.device != torch.device(device):
+            self._buf = buf = workspace(nbytes, device, zero_prefix=counter_bytes)
+        elif counter_bytes > self._zero:
+            buf[:counter_bytes].zero_()
+        self._zero = int(counter_bytes)
+        return buf
+
+
 def default_sm_scale(d: int) -> float:
     return 1.0 / math.sqrt(d)

@@ -350,14 +350,9 @@ class KIVIFusedCache(KIVICache):
         nbytes = lib.akv_decode_workspace_bytes(ctypes.byref(a))
         if nbytes < 0:
             nat.check(lib.akv_decode_attn(ctypes.byref(a), None), "KIVIFusedCache.fused_attention")
-        ctr = lib.akv_decode_counter_bytes(ctypes.byref(a))
-        ws, zeroed = self._ws.get(q.device, (None, 0))
-        if ws is None or ws.numel() < nbytes:
-            ws, zeroed = nat.workspace(nbytes, q.device, zero_prefix=ctr), ctr
-        elif ctr > zeroed:
-            ws[:ctr].zero_()
-            zeroed = ctr
-        self._ws[q.device] = (ws, zeroed)
+        # one workspace per device, shared by every layer, batch size and query length
+        ws = self._ws.setdefault(q.device, nat.DecodeWorkspace()).get(
+            nbytes, lib.akv_decode_counter_bytes(ctypes.byref(a)), q.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
         nat.check(lib.akv_decode_attn(ctypes.byref(a), nat.stream_of(q)), "KIVIFusedCache.fused_attention")
         return out

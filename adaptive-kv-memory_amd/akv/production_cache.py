@@ -94,8 +94,7 @@ class ProductionLayerCache:
         self._hot_v_contig = torch.zeros_like(self._hot_k_contig)
         self._hot_contig_len = 0
         self._seq_len = 0
-        self._ws: Optional[torch.Tensor] = None  # decode workspace, reused across calls
-        self._ws_zeroed = 0
+        self._ws = nat.DecodeWorkspace()  # decode workspace, reused across calls
 
     @property
     def hot_len(self) -> int:
@@ -220,23 +219,11 @@ class ProductionLayerCache:
         nbytes = lib.akv_decode_workspace_bytes(ctypes.byref(a))
         if nbytes < 0:
             nat.check(lib.akv_decode_attn(ctypes.byref(a), None), "ProductionCache.fused_attention")
-        ws = self._decode_workspace(nbytes, lib.akv_decode_counter_bytes(ctypes.byref(a)), q.device)
+        # the layer's workspace, kept across calls (calls on one layer are ordered on one stream)
+        ws = self._ws.get(nbytes, lib.akv_decode_counter_bytes(ctypes.byref(a)), q.device)
         a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
         nat.check(lib.akv_decode_attn(ctypes.byref(a), nat.stream_of(q)), "ProductionCache.fused_attention")
         return out
-
-    def _decode_workspace(self, nbytes: int, counter_bytes: int, device) -> torch.Tensor:
-        """The layer's decode workspace, kept across calls: a completed call leaves its split
-        counters at zero, so the counter prefix is zeroed only when the buffer is new or the
-        region grows.  Calls on one layer must be ordered on one stream (they share it)."""
-        ws = self._ws
-        if ws is None or ws.numel() < nbytes or ws.device != torch.device(device):
-            self._ws = nat.workspace(nbytes, device, zero_prefix=counter_bytes)
-            self._ws_zeroed = counter_bytes
-        elif counter_bytes > self._ws_zeroed:
-            ws[:counter_bytes].zero_()
-            self._ws_zeroed = counter_bytes
-        return self._ws
 
 
 class ProductionCache:

@@ -423,8 +423,12 @@ std::mutex g_scratch_mu;
 char *g_scratch_ptr[kMaxDevices] = {};
 
 // The address of this device's `scratch`, found once per device (with that device
-// current) by hipGetSymbolAddress; on that first call the counter region is cleared
-// by a kernel on `stream` (no memset node, so a graph capture may contain the call).
+// current) by hipGetSymbolAddress.  The counter region starts zero: the array is
+// zero-initialised when the code object is loaded, and every completed call leaves its
+// counters zero.  On the first call on a device the region is also cleared by a kernel
+// on `stream` -- unless that stream is being captured, where the clear would only become
+// a graph node that runs at replay (after eager calls made before it); such a first call
+// relies on the load-time zero initialisation alone.
 int scratch_base(void *stream, char **out) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -442,8 +446,13 @@ int scratch_base(void *stream, char **out) {
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
         if (!ptr) return fail(AKV_E_HIP, "hipGetSymbolAddress(scratch) returned NULL");
-        e = akv::zero_fill_launch(ptr, kScratchCtrBytes, (hipStream_t)stream);
-        if (e != hipSuccess) return hip_fail(e, "scratch counter clear");
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing((hipStream_t)stream, &cap);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+        if (cap == hipStreamCaptureStatusNone) {
+            e = akv::zero_fill_launch(ptr, kScratchCtrBytes, (hipStream_t)stream);
+            if (e != hipSuccess) return hip_fail(e, "scratch counter clear");
+        }
         g_scratch_ptr[dev] = (char *)ptr;
     }
     *out = g_scratch_ptr[dev];

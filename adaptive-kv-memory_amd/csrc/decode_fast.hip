@@ -563,8 +563,10 @@ void decode_fast_kernel(const DecodeParams p) {
             //      and read back per MFMA step; the fast paths hold when no -1024 s overflows
             //      (K and V scales of the unit).  LEG: the lane's 32 channels lie in one group,
             //      so its token has one (s, z) per half, read from the slot; the value is
-            //      round16(c s + z) in one fma (the reference dequantizes this layout in fp32 and
-            //      rounds once), and the symmetric branch round16((c - half_max) s).
+            //      round16(c s + z) in one fma, rounded once in fp16 (the reference rounds c s + z
+            //      in fp32 and then to fp16, so a value may differ by one fp16 ulp at an fp32-rounded
+            //      tie: within the attention tolerance), and the symmetric branch
+            //      round16((c - half_max) s).
             bool kfast = true;
             h2 ls[2] = {}, lz[2] = {};
             if constexpr (LEG) {

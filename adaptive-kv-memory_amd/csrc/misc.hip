@@ -157,12 +157,14 @@ __global__ __launch_bounds__(kImpTile) void importance_kernel(const ImportancePa
 }
 
 // Without key pooling: a workgroup owns 64 keys and its RG waves split the (batch x
-// head) rows into RG contiguous ranges (every query row m >= m0 of them), 8 loads in
-// flight per lane; the RG partial sums are added in range order.  The row loads of a
-// wave cover 64 consecutive keys (256 coalesced bytes at fp32).  Sum order: over the
-// rows of a range, then over the ranges, then divided by B*H -- the same sum as
-// key_importance in another association (fp32 rounding differs in the last bits).
-// RG = 16 when there are too few key tiles to fill the GPU with RG = 4.
+// head) rows into RG contiguous ranges, 8 loads in flight per lane.  The row loads of
+// a wave cover 64 consecutive keys (256 coalesced bytes at fp32).  Sum order, per
+// query row m >= m0: over the rows of a range, then over the ranges in range order,
+// then divided by B*H; the per-query means are then added in query order -- the
+// reference's association (mean over batch and heads, then the sum over queries),
+// with the (batch, head) sum itself in another order than torch's reduction (fp32
+// rounding may differ in the last bits).  RG = 16 when there are too few key tiles to
+// fill the GPU with RG = 4.
 constexpr int kImpKeys = 64;
 template <int RG>
 __global__ __launch_bounds__(64 * RG) void importance_rows_kernel(const ImportanceParams p) {
@@ -171,9 +173,10 @@ __global__ __launch_bounds__(64 * RG) void importance_rows_kernel(const Importan
     const int64_t n = (int64_t)blockIdx.x * kImpKeys + lane;
     const int64_t bhn = p.B * p.H, per = (bhn + RG - 1) / RG;
     const int64_t bh0 = min(bhn, per * w), bh1 = min(bhn, bh0 + per);
-    float acc = 0.f;
-    if (n < p.N) {
-        for (int64_t m = p.m0; m < p.M; ++m) {
+    float imp = 0.f;  // wave 0: the sum over queries of the per-query means
+    for (int64_t m = p.m0; m < p.M; ++m) {
+        float acc = 0.f;
+        if (n < p.N) {
             int64_t bh = bh0;
             for (; bh + 8 <= bh1; bh += 8) {
                 float x[8];
@@ -184,14 +187,18 @@ __global__ __launch_bounds__(64 * RG) void importance_rows_kernel(const Importan
             }
             for (; bh < bh1; ++bh) acc += load_as_f32(p.attn, (bh * p.M + m) * p.N + n, p.attn_dt);
         }
-    }
-    part[w][lane] = acc;
-    __syncthreads();
-    if (w != 0 || n >= p.n_scores) return;
-    float tot = 0.f;
+        part[w][lane] = acc;
+        __syncthreads();
+        if (w == 0) {
+            float tot = 0.f;
 #pragma unroll
-    for (int r = 0; r < RG; ++r) tot += part[r][lane];
-    const float imp = n < p.N ? tot / (float)bhn : 0.f;
+            for (int r = 0; r < RG; ++r) tot += part[r][lane];
+            imp += tot / (float)bhn;
+        }
+        __syncthreads();  // part is rewritten for the next query row
+    }
+    if (w != 0 || n >= p.n_scores) return;
+    if (n >= p.N) imp = 0.f;
     float sc = p.scores[n] * p.decay;
     sc = sc + imp;
     p.scores[n] = sc;

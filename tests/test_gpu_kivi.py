@@ -130,3 +130,22 @@ def test_fused_attention_matches_oracle(B, H, Hq, M, bits, gs):
     ref, _ = oatt.attention_fp32(q.astype(np.float16), ok.astype(np.float16), ov.astype(np.float16), sm_scale=0.04,
                                  return_weights=False)
     assert_close_attn(cache.fused_attention(to_dev(q), 0, sm_scale=0.04), ref)
+
+
+def test_fused_attention_counter_region_shrinks_then_grows():
+    """One workspace per device serves every call: query lengths 32 -> 1 -> 32 on 16
+    heads halve and then double its split-counter region; each output is checked."""
+    from akv.baselines import KIVIFusedCache, KIVIFusedConfig
+    announce("KIVI fused_attention M=32,1,32 (shared workspace counter region)")
+    cache = KIVIFusedCache(KIVIFusedConfig(key_bits=2, value_bits=2, group_size=128, residual_length=32))
+    orc = KIVIOracle(2, 2, 128, 32, fused=True)
+    rng = np.random.default_rng(5)
+    B, H, D = 2, 16, 128
+    k, v = _kv(rng, B, H, 700, D)
+    cache.update(to_dev(k, torch.float16), to_dev(v, torch.float16), 0)
+    ok, ov = orc.update(k, v, 0)
+    for M in (32, 1, 32, 3, 32):
+        q = rng.standard_normal((B, H, M, D)).astype(np.float32)
+        ref, _ = oatt.attention_fp32(q.astype(np.float16), ok.astype(np.float16), ov.astype(np.float16),
+                                     return_weights=False)
+        assert_close_attn(cache.fused_attention(to_dev(q), 0), ref)

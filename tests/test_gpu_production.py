@@ -142,3 +142,24 @@ def test_hot_only_and_errors():
         ProductionLayerCache(_config(3, 64, warm_quantizer="turbo"), 0)
     with pytest.raises(ValueError, match="2, 4 or 8"):
         ProductionLayerCache(_config(3, 64), 0)
+
+
+def test_fused_attention_counter_region_shrinks_then_grows():
+    """Query lengths 32 -> 1 -> 32 on 32 heads: the split-counter region of the layer's
+    reused workspace halves, the short call writes partials over its tail, and the next
+    long call must clear it again (each output checked against the oracle)."""
+    from akv.production_cache import ProductionCache
+    announce("ProductionCache fused_attention M=32,1,32 (workspace counter region)")
+    cfg = _config(4, 64, num_layers=1, num_heads=32, hot_budget=48, warm_budget=256)
+    cache, orc = ProductionCache(cfg), _oracle(cfg)
+    rng = np.random.default_rng(11)
+    H, D = cfg.num_heads, cfg.head_dim
+    k, v = _rows(rng, H, 200, D), _rows(rng, H, 200, D)
+    attn = _attn(rng, H, 200, 200)
+    cache.update(to_dev(k[None], torch.float16), to_dev(v[None], torch.float16), 0, to_dev(attn))
+    orc.update(k, v, 0, attn)
+    _check_view(cache, orc, 0, "prefill")
+    assert cache._layers[0].warm_len > 0
+    for M in (32, 1, 32, 5, 32):
+        q = rng.standard_normal((1, H, M, D)).astype(np.float32)
+        assert_close_attn(cache.fused_attention(to_dev(q), 0), orc.attention(q, 0))

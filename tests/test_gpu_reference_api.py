@@ -163,6 +163,13 @@ def test_fused_importance_update_kats():
         s0 = rng.random(n).astype(np.float32)
         got = akv.fused_importance_update(to_dev(a), to_dev(s0.copy()), decay=0.8)
         np.testing.assert_allclose(got.cpu().numpy(), oimp.fused_importance_update(a, s0, 0.8), rtol=1e-6, atol=1e-7)
+    # non-dyadic weights over many (batch, head) rows and 3 queries (16 waves per key tile):
+    # the per-query mean, then the sum over queries, as the reference associates it
+    a = rng.random((8, 12, 3, 300)).astype(np.float32)
+    a /= a.sum(-1, keepdims=True)
+    s0 = rng.random(300).astype(np.float32)
+    got = akv.fused_importance_update(to_dev(a), to_dev(s0.copy()), decay=0.9)
+    np.testing.assert_allclose(got.cpu().numpy(), oimp.fused_importance_update(a, s0, 0.9), rtol=1e-6, atol=1e-8)
 
 
 def test_importance_scorer_accumulate():

@@ -66,3 +66,21 @@ def test_workload_shapes():
     # two channels per head scaled x10
     std = k.float().std(dim=2)[0]
     assert int((std > 5).sum()) == 4
+
+
+def test_decode_workspace_tracks_the_last_counter_region():
+    """A reused decode workspace: after a call only that call's counter prefix is known
+    to be zero (its partials follow it), so a later call with a larger counter region
+    must find it cleared again.  Runs on host memory; the 'call' is simulated by
+    writing partial bytes after the counter prefix."""
+    from akv._native import DecodeWorkspace
+    ws = DecodeWorkspace()
+    buf = ws.get(4096, 512, "cpu")
+    assert int(buf[:512].sum()) == 0
+    buf = ws.get(4096, 256, "cpu")  # a smaller region: no clearing needed
+    buf[256:1024] = 7  # that call's partials land over the old counter tail
+    buf = ws.get(4096, 512, "cpu")
+    assert int(buf[:512].sum()) == 0, "the grown counter region was not cleared"
+    buf[512:] = 3
+    assert ws.get(4096, 512, "cpu") is buf and int(buf[:512].sum()) == 0
+    assert ws.get(8192, 256, "cpu").numel() >= 8192  # grows when a call needs more bytes
