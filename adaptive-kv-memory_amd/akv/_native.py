@@ -127,6 +127,7 @@ EXPORTS = (
     "akv_quant_pack", "akv_dequant_unpack",
     "akv_bitpack", "akv_bitunpack", "akv_importance_update",
     "akv_prefill_workspace_bytes", "akv_prefill_attn", "akv_select_demote", "akv_stream_read",
+    "akv_timeline_words", "akv_timeline_fetch", "akv_timeline_clear",
 )
 STRUCTS = (WarmDesc, DecodeArgs, QuantArgs, DequantArgs, ImportanceArgs, PrefillArgs)
 
@@ -173,6 +174,12 @@ def load() -> ctypes.CDLL:
     lib.akv_select_demote.argtypes = [_vp, _i64, _i64, _i64, _i32, _i32, _vp, _vp]
     lib.akv_stream_read.restype = ctypes.c_int
     lib.akv_stream_read.argtypes = [_vp, _i64, _vp, _vp]
+    lib.akv_timeline_words.restype = _i64
+    lib.akv_timeline_words.argtypes = []
+    lib.akv_timeline_fetch.restype = ctypes.c_int
+    lib.akv_timeline_fetch.argtypes = [_vp, _i64]
+    lib.akv_timeline_clear.restype = ctypes.c_int
+    lib.akv_timeline_clear.argtypes = [_vp]
     if lib.akv_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH} has ABI {lib.akv_abi_version()}, expected {ABI_VERSION}")
     for i, st in enumerate(STRUCTS):

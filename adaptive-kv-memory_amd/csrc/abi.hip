@@ -387,6 +387,10 @@ int decode_run(const akv_decode_args *a, const Plan &pl, char *ctr, char *ws, vo
     p.N = pl.N;
     p.n_wsplit = pl.n_wsplit; p.n_hsplit = pl.n_hsplit; p.nsplit = pl.nsplit;
     p.wsplit_len = pl.wsplit_len; p.hsplit_len = pl.hsplit_len;
+    p.fd_nsplit = akv::make_fast_div((uint32_t)pl.nsplit);
+    p.fd_hkv = akv::make_fast_div((uint32_t)a->Hkv);
+    p.fd_nchunk = akv::make_fast_div((uint32_t)pl.nchunk);
+    p.fd_m = akv::make_fast_div((uint32_t)a->M);
     p.out = (_Float16 *)a->out;
     p.attn_out = a->attn_weights;
     p.stash = a->attn_weights ? a->attn_weights : (a->scores ? stash_ws : nullptr);
@@ -691,6 +695,25 @@ int akv_prefill_attn(const akv_prefill_args *a, void *stream) {
     p.nchunk = pl.nchunk; p.prows = pl.prows;
     hipError_t e = akv::prefill_launch(p, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
+    return ok();
+}
+
+int64_t akv_timeline_words(void) { return akv::decode_fast_timeline_words(); }
+
+int akv_timeline_fetch(uint64_t *host, int64_t words) {
+    if (akv::decode_fast_timeline_words() == 0)
+        return fail(AKV_E_UNSUPPORTED, "this build records no timeline (build it with make timeline)");
+    if (!host || words < 0) return fail(AKV_E_INVALID, "bad timeline buffer");
+    hipError_t e = akv::decode_fast_timeline_fetch((unsigned long long *)host, words);
+    if (e != hipSuccess) return hip_fail(e, "timeline fetch");
+    return ok();
+}
+
+int akv_timeline_clear(void *stream) {
+    if (akv::decode_fast_timeline_words() == 0)
+        return fail(AKV_E_UNSUPPORTED, "this build records no timeline (build it with make timeline)");
+    hipError_t e = akv::decode_fast_timeline_clear((hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "timeline clear");
     return ok();
 }
 

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fastdiv.h"
+
 namespace akv {
 
 struct DecodeParams {
@@ -52,6 +54,9 @@ struct DecodeParams {
     float decay;
     // fast path (decode_fast.hip): bytes of one LDS ring slot
     int slot_bytes;
+    // fast path: the workgroup id split into (split, kv-head, batch x row chunk) and a
+    // row of a chunk into (query head, query position) without integer division
+    FastDiv fd_nsplit, fd_hkv, fd_nchunk, fd_m;
 };
 
 // Launch split + reduce (+ weights/importance) kernels.  `sym_src` = {meta dtype, count}
@@ -76,5 +81,9 @@ bool decode_fast_meta_aligned(int64_t rows_per_head, int Gv, int64_t heads);
 int64_t decode_fast_lds_bytes(int64_t slot_bytes, int n_out);
 int decode_fast_waves(int n_out);
 hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, int wk, hipStream_t s);
+// Per-wave timeline of the fast kernel (timeline build only; 0 words / hipErrorNotSupported otherwise).
+int64_t decode_fast_timeline_words();
+hipError_t decode_fast_timeline_fetch(unsigned long long *host, int64_t words);
+hipError_t decode_fast_timeline_clear(hipStream_t s);
 
 }  // namespace akv

@@ -69,6 +69,29 @@
 
 namespace akv {
 
+// ---- per-wave timeline, recorded only by the timeline build of the library
+// (make timeline: -DAKV_TIMELINE).  Words per wave (blockIdx.x * waves + wave):
+// 0 start, 1 first item's data in LDS, 2 warm items done, 3 all items done,
+// 4 partial written and acknowledged, 5 arrival counted (ticks x 4 + role:
+// 0 not last, 1 last, 2 last with every partial from its XCD), 6 merge done (wave 0
+// of the merging workgroup), 7 items taken, 8 ticks waiting for ring data, 9 XCC id,
+// 10 first load issued, 13 start barrier passed.  Times are s_memrealtime ticks
+// (100 MHz).  The values carry threadIdx.x & 1 (0 on lane 0) so that they live in
+// vector registers and leave through vector stores.
+#ifdef AKV_TIMELINE
+constexpr int kTlWords = 16, kTlCap = 1 << 17;
+__device__ unsigned long long g_akv_timeline[kTlCap];
+#define AKV_TL(k, v)                                                                      \
+    do {                                                                                  \
+        if (lane == 0 && tl_base + (k) < kTlCap)                                          \
+            g_akv_timeline[tl_base + (k)] = (unsigned long long)(v) + (threadIdx.x & 1u); \
+    } while (0)
+#define AKV_TL_NOW() __builtin_amdgcn_s_memrealtime()
+#else
+#define AKV_TL(k, v) ((void)0)
+#define AKV_TL_NOW() 0ull
+#endif
+
 namespace {
 
 constexpr int kD = 128;
@@ -98,7 +121,7 @@ template <int OUT> struct FastCfg {
 constexpr int kLdsCap = 160 * 1024;  // LDS of one CU
 constexpr int kKmetaBytes = 3 * 4 * 16 * 4;  // [s | n | z][group][pair] u32
 constexpr int kHotLoads = 4;         // 16 tokens x 256 B = 4 KiB = 4 wave loads
-constexpr int kQldsBytes = 4 * 64 * 16;  // Q operand of the workgroup
+constexpr int kQldsBytes = 16 * kD * 2;  // the workgroup's 16 query rows (fp16)
 constexpr int kAccRow = kD + 4;      // fp32 row of the end-of-split merge in LDS (the pad spreads a
                                      // wave's 64 row/chunk writes over the banks)
 constexpr int kMaxOut = 4;            // outlier channels per block the fast kernel takes
@@ -283,24 +306,32 @@ void decode_fast_kernel(const DecodeParams p) {
         const int nwg = (int)gridDim.x;
         if (nwg % 8 == 0) wid = (wid % 8) * (nwg / 8) + wid / 8;
     }
-    const int split = wid % p.nsplit, kvh = (wid / p.nsplit) % p.Hkv;
-    const int bz = wid / (p.nsplit * p.Hkv);
-    const int b = bz / p.nchunk, chunk = bz % p.nchunk;
+#ifdef AKV_TIMELINE
+    const int tl_base = ((int)blockIdx.x * NW + wave) * kTlWords;
+    AKV_TL(0, AKV_TL_NOW());
+    unsigned long long tl_wait = 0;
+    int tl_items = 0;
+#endif
+    // (split, kv-head, batch x row chunk) of the workgroup, by multiply-shift division
+    const int q1 = (int)fast_div((uint32_t)wid, p.fd_nsplit);
+    const int split = wid - q1 * p.nsplit;
+    const int bz = (int)fast_div((uint32_t)q1, p.fd_hkv);
+    const int kvh = q1 - bz * p.Hkv;
+    const int b = (int)fast_div((uint32_t)bz, p.fd_nchunk), chunk = bz - b * p.nchunk;
     const int row0 = chunk * 16;
     const int nrows = min(16, p.R - row0);
     const int slot_bytes = p.slot_bytes;
     unsigned char *ring = smem + wave * (NS * slot_bytes + kKmetaBytes);
     unsigned char *kmeta = ring + NS * slot_bytes;
     unsigned *work = (unsigned *)(smem + NW * (NS * slot_bytes + kKmetaBytes));  // item counter
-    // Q operand of the QK MFMAs, [step][lane] x 16 B, shared by the waves
-    u4 *qlds = (u4 *)(smem + NW * (NS * slot_bytes + kKmetaBytes) + 16);
     // the 16 query rows in natural channel order (fp16): outlier-channel corrections
-    const _Float16 *qn_lds = (const _Float16 *)((unsigned char *)qlds + kQldsBytes);
+    _Float16 *qn_lds = (_Float16 *)(smem + NW * (NS * slot_bytes + kKmetaBytes) + 16);
 
     const int r = row0 + col;
     const int row_valid = col < nrows;
     const int rc = row_valid ? r : row0;
-    const int hq = kvh * p.g + rc / p.M, mq = rc % p.M;
+    const int rq = (int)fast_div((uint32_t)rc, p.fd_m);
+    const int hq = kvh * p.g + rq, mq = rc - rq * p.M;
     const int64_t strow = ((int64_t)(b * p.Hq + hq) * p.M + mq) * p.N;
     const int64_t bh = (int64_t)b * p.Hkv + kvh;
     const float sl2 = p.scale_log2;
@@ -405,46 +436,20 @@ void decode_fast_kernel(const DecodeParams p) {
         else if (k == kHotK) issue_hot(rkh, slot, lane, id);
         else if (k == kHotV) issue_hot(rvh, slot, lane, id);
     };
-    // Q operand (B of QK): lane = (row col, channel group grp), in the channel
-    // order the warm code pairs come out in (hot K is permuted to match).  Wave 0
-    // stages it in LDS for the workgroup before it takes its first unit.
-    if (wave == 0) {
-        const u4 *qrow = (const u4 *)(p.q + ((int64_t)(b * p.Hq + hq) * p.M + mq) * kD + 32 * grp);
-        uint32_t nat[16], pairs[16];
-#pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-            const u4 x = qrow[q4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const uint32_t xe = x[e];
-                nat[4 * q4 + e] = xe;
-            }
-        }
-        hot_k_pairs<BK>(nat, pairs);
-#pragma unroll
-        for (int st = 0; st < KSTEPS; ++st)
-            qlds[st * 64 + lane] = (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]};
-        if (OUT) {
-            u4 *qn = (u4 *)qn_lds + col * 16 + grp * 4;
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) qn[q4] = (u4){nat[4 * q4], nat[4 * q4 + 1], nat[4 * q4 + 2], nat[4 * q4 + 3]};
-        }
-    }
-    // Only the first slot is filled up front: every wave's first unit is in
-    // the memory queue before any wave's second, so compute starts as soon as
-    // a first unit lands; the other slots fill once it has (loop, first pass).
+    // Only the first slot is filled up front, with the 16 query rows of the workgroup
+    // (4 KiB, rows past the chunk read as zeros) in the last slot beside it: every wave's
+    // first unit is in the memory queue before any wave's second, so compute starts as
+    // soon as a first unit lands; the other slots fill once it has.
     next_unit(qk[0], qi[0]);
+    AKV_TL(10, AKV_TL_NOW());
     issue(qk[0], qi[0], ring);
+    {
+        // the chunk's rows r are query rows (kvh * g + r / M, r % M): consecutive in q
+        const int64_t qrow0 = ((int64_t)(b * p.Hq + kvh * p.g) * p.M + row0) * kD;
+        issue_hot(rsrc4(p.q + qrow0, (uint32_t)(nrows * kD * 2)), ring + (NS - 1) * slot_bytes, lane, 0);
+    }
 #pragma unroll
     for (int s2 = 1; s2 < NS; ++s2) qk[s2] = kNone;
-    bool primed = false;
-    __syncthreads();  // Q operand and item counter in LDS before any wave uses them
-    // the query operand stays in registers for the whole range (16 VGPRs): one LDS read per
-    // MFMA step less in every unit
-    h8 qreg[KSTEPS];
-#pragma unroll
-    for (int st = 0; st < KSTEPS; ++st) qreg[st] = __builtin_bit_cast(h8, qlds[st * 64 + lane]);
-    auto qop = [&](int st) { return qreg[st]; };
 
     Soft stt;
     stt.m2 = -INFINITY;
@@ -468,10 +473,50 @@ void decode_fast_kernel(const DecodeParams p) {
     const int v_lane = L::VC + 4 * grp * L::VR + (BV == 3 ? 3 * col : BV == 4 ? 4 * col : 2 * col);
     const int vm_lane = (4 * grp * NG + gv) * 2;
 
+    __syncthreads();  // the item counter is in LDS before any wave claims from it
+    AKV_TL(13, AKV_TL_NOW());
+    wait_vm<0>();  // the first item and the query rows have landed
+    AKV_TL(1, AKV_TL_NOW());
+    // Q operand (B of QK): lane = (row col, channel group grp), in the channel order the
+    // warm code pairs come out in (hot K is permuted to match); it stays in registers for
+    // the whole range (16 VGPRs).  The outlier variants also keep the rows in natural
+    // channel order in LDS (every wave writes the same values there).
+    h8 qreg[KSTEPS];
+    {
+        const unsigned char *qs = ring + (NS - 1) * slot_bytes;
+        uint32_t nat[16], pairs[16];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+            const u4 x = *(const u4 *)(qs + col * 256 + grp * 64 + 16 * q4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t xe = x[e];
+                nat[4 * q4 + e] = xe;
+            }
+        }
+        hot_k_pairs<BK>(nat, pairs);
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st)
+            qreg[st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
+        if (OUT) {
+            u4 *qn = (u4 *)qn_lds + col * 16 + grp * 4;
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) qn[q4] = (u4){nat[4 * q4], nat[4 * q4 + 1], nat[4 * q4 + 2], nat[4 * q4 + 3]};
+        }
+    }
+    auto qop = [&](int st) { return qreg[st]; };
+    // every read of the query slot has returned before the slot is refilled
+    wait_lgkm0();
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int s2 = 1; s2 < NS; ++s2) {
+        next_unit(qk[s2], qi[s2]);
+        issue(qk[s2], qi[s2], ring + s2 * slot_bytes);
+    }
+
     h4 hot_p = {};  // P of the hot tile whose K half was just processed
     int head = 0;  // ring slot of the oldest queue entry
-    // Wait for the head slot's loads (the younger slots' loads may stay in flight);
-    // on the first item, issue the other slots once the first has landed.
+    // Wait for the head slot's loads (the younger slots' loads may stay in flight).
     auto wait_head = [&]() {
         int nwy = 0, nhy = 0;
 #pragma unroll
@@ -480,14 +525,6 @@ void decode_fast_kernel(const DecodeParams p) {
             nhy += qk[i] == kHotK || qk[i] == kHotV;
         }
         wait_younger<NLW, NLH, NS - 1>(nwy, nhy);
-        if (!primed) {
-            primed = true;
-#pragma unroll
-            for (int s2 = 1; s2 < NS; ++s2) {
-                next_unit(qk[s2], qi[s2]);
-                issue(qk[s2], qi[s2], ring + s2 * slot_bytes);
-            }
-        }
     };
     // Every read of the head slot has landed: refill it with the youngest entry.
     auto advance = [&](unsigned char *slot) {
@@ -508,7 +545,16 @@ void decode_fast_kernel(const DecodeParams p) {
     while (qk[0] == kWarm) {
         const int id = qi[0];
         unsigned char *slot = ring + head * slot_bytes;
+#ifdef AKV_TIMELINE
+        {
+            const unsigned long long t0 = AKV_TL_NOW();
+            wait_head();
+            tl_wait += AKV_TL_NOW() - t0;
+            ++tl_items;
+        }
+#else
         wait_head();
+#endif
         if (NG < 4 && id * kUnit + kUnit > nw) {
             // the tail unit: meta rows past the tier's last token may hold bytes from outside it
             const int t = lane & 31;
@@ -896,11 +942,21 @@ void decode_fast_kernel(const DecodeParams p) {
         }
         advance(slot);
     }
+    AKV_TL(2, AKV_TL_NOW());
     while (qk[0] != kNone) {
         const int k = qk[0];
         const int id = qi[0];
         unsigned char *slot = ring + head * slot_bytes;
+#ifdef AKV_TIMELINE
+        {
+            const unsigned long long t0 = AKV_TL_NOW();
+            wait_head();
+            tl_wait += AKV_TL_NOW() - t0;
+            ++tl_items;
+        }
+#else
         wait_head();
+#endif
         if (k == kHotK) {
             // ---- hot K tile: 16 tokens x 256 B; lane = (token col, 32 channels of group grp)
             uint32_t nat[16], pairs[16];
@@ -946,6 +1002,16 @@ void decode_fast_kernel(const DecodeParams p) {
 
     // ---- merge the waves (the ring memory is reused): every wave rescales its
     //      rows to the workgroup maximum, then the 12 states are summed
+#ifdef AKV_TIMELINE
+    AKV_TL(3, AKV_TL_NOW());
+    AKV_TL(7, tl_items);
+    AKV_TL(8, tl_wait);
+    {
+        unsigned xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+        AKV_TL(9, xcc & 7u);
+    }
+#endif
     wait_vm<0>();
     stt.l = wsum16(stt.l);
     __syncthreads();
@@ -1008,6 +1074,7 @@ void decode_fast_kernel(const DecodeParams p) {
     //      it.  The merge reads them from its own L2 when every partial came from
     //      its XCD, else from the coherence point.  The counter returns to zero.
     wait_vm<0>();
+    AKV_TL(4, AKV_TL_NOW());
     __syncthreads();
     if (tid == 0) {
         // one byte per XCD counts the partials written from it
@@ -1024,6 +1091,7 @@ void decode_fast_kernel(const DecodeParams p) {
     }
     __syncthreads();
     const unsigned role = *work;
+    AKV_TL(5, AKV_TL_NOW() * 4ull + role);
     if (role == 0u) return;
     if (tid == 0) __hip_atomic_store(p.split_ctr + bhc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid >= nrows * (kD / 4)) return;
@@ -1034,10 +1102,12 @@ void decode_fast_kernel(const DecodeParams p) {
         if (role == 2u) merge_partials<1>(prs, p.nsplit, pstride, rr, c4, M, L, a);    // L2-coherent loads
         else merge_partials<kSc1>(prs, p.nsplit, pstride, rr, c4, M, L, a);            // device-coherent loads
         const int r = row0 + rr;
-        const int h = kvh * p.g + r / p.M, m = r % p.M;
+        const int rq2 = (int)fast_div((uint32_t)r, p.fd_m);
+        const int h = kvh * p.g + rq2, m = r - rq2 * p.M;
         const int64_t row = (int64_t)(b * p.Hq + h) * p.M + m;
         const h4 ov = {(_Float16)(a[0] / L), (_Float16)(a[1] / L), (_Float16)(a[2] / L), (_Float16)(a[3] / L)};
         *(h4 *)(p.out + row * kD + 4 * c4) = ov;
+        if (tid == 0) AKV_TL(6, AKV_TL_NOW());
         if (c4 == 0 && p.rowstats) {
             p.rowstats[2 * row] = M;
             p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
@@ -1064,8 +1134,8 @@ static_assert(kWavesOut * (kNSOut * 4096 + kKmetaBytes) >= (2 * kWavesOut * 16 +
               "merge area overlaps the item counter");
 int64_t decode_fast_lds_bytes(int64_t slot, int n_out) {
     const int nw = n_out > 1 ? kWavesOut : kWaves, ns = n_out > 1 ? kNSOut : kNS;
-    // Q operand, plus the natural-order query rows for the outlier corrections
-    const int64_t ring = nw * (ns * slot + kKmetaBytes) + 16 + (n_out > 0 ? 2 : 1) * kQldsBytes;
+    // the item counter, plus the natural-order query rows for the outlier corrections
+    const int64_t ring = nw * (ns * slot + kKmetaBytes) + 16 + (n_out > 0 ? kQldsBytes : 0);
     const int64_t merge = (int64_t)(2 * nw * 16 + nw * 16 * kAccRow) * 4;
     return ring > merge ? ring : merge;
 }
@@ -1133,6 +1203,36 @@ static hipError_t launch_fast_ng(const DecodeParams &p, hipStream_t s) {
     if (p.Gv == 64) return launch_fast<BK, BV, 2, LEG>(p, s);
     if (p.Gv == 128) return launch_fast<BK, BV, 1, LEG>(p, s);
     return hipErrorInvalidValue;
+}
+
+// Timeline of the last launches (timeline build only): copy / clear the per-wave words.
+int64_t decode_fast_timeline_words() {
+#ifdef AKV_TIMELINE
+    return kTlCap;
+#else
+    return 0;
+#endif
+}
+hipError_t decode_fast_timeline_fetch(unsigned long long *host, int64_t words) {
+#ifdef AKV_TIMELINE
+    if (words > kTlCap) words = kTlCap;
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(g_akv_timeline), (size_t)words * 8, 0, hipMemcpyDeviceToHost);
+#else
+    (void)host;
+    (void)words;
+    return hipErrorNotSupported;
+#endif
+}
+hipError_t decode_fast_timeline_clear(hipStream_t s) {
+#ifdef AKV_TIMELINE
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_akv_timeline));
+    if (e != hipSuccess) return e;
+    return hipMemsetAsync(ptr, 0, sizeof(unsigned long long) * kTlCap, s);
+#else
+    (void)s;
+    return hipErrorNotSupported;
+#endif
 }
 
 hipError_t decode_fast_split_launch(const DecodeParams &p, int kb, int vb, int wk, hipStream_t s) {

@@ -328,6 +328,16 @@ int64_t akv_struct_size(int32_t which);
  * equals a sentinel.  Its time beside a kernel's, over the same byte count, is the streaming
  * roofline the benchmark reports. */
 int akv_stream_read(const void *data, int64_t bytes, uint32_t *sink, void *stream);
+/* Measurement helpers with no counterpart in the reference: the per-wave timeline of the
+ * fast decode kernel, recorded only by the timeline build of the library (`make timeline`,
+ * compiled with -DAKV_TIMELINE; 16 words per wave, s_memrealtime ticks at 100 MHz, the
+ * word meanings are listed in csrc/decode_fast.hip).  akv_timeline_words returns the
+ * number of words the build records (0 in the normal build, where fetch and clear return
+ * AKV_E_UNSUPPORTED).  fetch copies the first `words` words to host memory (synchronous);
+ * clear zeroes them on `stream`. */
+int64_t akv_timeline_words(void);
+int akv_timeline_fetch(uint64_t *host, int64_t words);
+int akv_timeline_clear(void *stream);
 
 #ifdef __cplusplus
 }

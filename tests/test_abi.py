@@ -61,6 +61,10 @@ def test_host_side_validation_without_gpu():
     assert lib.akv_stream_read(None, 32, None, None) == nat.AKV_E_INVALID
     assert lib.akv_stream_read(ctypes.c_void_p(8), 32, ctypes.c_void_p(16), None) == nat.AKV_E_ALIGN
     assert lib.akv_stream_read(None, 0, None, None) == nat.AKV_OK
+    # the normal build records no decode timeline (the timeline build does: make timeline)
+    assert lib.akv_timeline_words() == 0
+    assert lib.akv_timeline_fetch(None, 0) == nat.AKV_E_UNSUPPORTED
+    assert lib.akv_timeline_clear(None) == nat.AKV_E_UNSUPPORTED
 
 
 def test_decode_shape_checks():
