@@ -75,7 +75,8 @@ namespace akv {
 // 4 partial written and acknowledged, 5 arrival counted (ticks x 4 + role:
 // 0 not last, 1 last, 2 last with every partial from its XCD), 6 merge done (wave 0
 // of the merging workgroup), 7 items taken, 8 ticks waiting for ring data, 9 XCC id,
-// 10 first load issued, 13 start barrier passed.  Times are s_memrealtime ticks
+// 10 first load issued, 11 waves merged in LDS, 12 merger's partial loads done (thread 0),
+// 13 start barrier passed.  Times are s_memrealtime ticks
 // (100 MHz).  The values carry threadIdx.x & 1 (0 on lane 0) so that they live in
 // vector registers and leave through vector stores.
 #ifdef AKV_TIMELINE
@@ -1043,6 +1044,7 @@ void decode_fast_kernel(const DecodeParams p) {
     const __amdgpu_buffer_rsrc_t prs = make_rsrc(p.part + bhc * p.nsplit * pstride, (uint32_t)(p.nsplit * pstride * 4));
     constexpr int kSc1 = 16;  // cache-policy bit sc1: coherent at device scope
     const int tid = threadIdx.x;
+    AKV_TL(11, AKV_TL_NOW());
     if (tid < nrows * (kD / 4)) {  // thread = (row, channel quad); 512 <= 64 * NW
         const int rr = tid / (kD / 4), c4 = tid % (kD / 4);
         f4 a = {0.f, 0.f, 0.f, 0.f};
@@ -1093,7 +1095,11 @@ void decode_fast_kernel(const DecodeParams p) {
     const unsigned role = *work;
     AKV_TL(5, AKV_TL_NOW() * 4ull + role);
     if (role == 0u) return;
-    if (tid == 0) __hip_atomic_store(p.split_ctr + bhc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The count returns to zero from the workgroup's last thread when that thread merges
+    // nothing (a merging wave would wait for this store with its loads: vmcnt counts stores
+    // and loads in issue order).
+    if (tid == (nrows * (kD / 4) < 64 * NW ? 64 * NW - 1 : 0))
+        __hip_atomic_store(p.split_ctr + bhc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid >= nrows * (kD / 4)) return;
     {
         const int rr = tid / (kD / 4), c4 = tid % (kD / 4);
@@ -1101,6 +1107,7 @@ void decode_fast_kernel(const DecodeParams p) {
         f4 a = {0.f, 0.f, 0.f, 0.f};
         if (role == 2u) merge_partials<1>(prs, p.nsplit, pstride, rr, c4, M, L, a);    // L2-coherent loads
         else merge_partials<kSc1>(prs, p.nsplit, pstride, rr, c4, M, L, a);            // device-coherent loads
+        if (tid == 0) AKV_TL(12, AKV_TL_NOW());
         const int r = row0 + rr;
         const int rq2 = (int)fast_div((uint32_t)r, p.fd_m);
         const int h = kvh * p.g + rq2, m = r - rq2 * p.M;
