@@ -226,10 +226,19 @@ class PackedKVArena:
 
 
 class PagedKVCache:
-    """Fixed-size pages of fp16 K/V with per-layer page tables
-    (akv/packed_layout.py:283-443).  ``k_pool`` / ``v_pool`` are
-    (max_pages, heads, page_size, head_dim) device tensors; the page tables and free
-    list are host bookkeeping; appends are slice writes into the pool."""
+    """The fp16 page pool of akv/packed_layout.py:283-443, kept on the device.
+
+    ``k_pool`` / ``v_pool`` hold ``max_pages`` pages of (heads, page_size, head_dim)
+    tokens.  Each layer's page table is a row of one int32 device tensor
+    (``num_layers`` x ``max_pages``): entry j is the page of the layer's tokens
+    j * page_size .. +page_size-1.  The host keeps only counts and the free list.
+
+    ``append`` takes the pages its tokens need off the end of the free list (the
+    reference's order), writes their ids into the table with one small copy, and then
+    scatters all N tokens into the pool with one indexed write per pool, whatever N;
+    ``get_kv`` gathers a layer's tokens with one indexed read per pool.  Freed pages are
+    zeroed, all of them with one fill per pool.  ``get_page_table`` returns the layer's
+    table as an int32 device tensor, as the reference does."""
 
     def __init__(self, num_layers: int, num_heads: int, head_dim: int, page_size: int = 16, max_pages: int = 4096,
                  dtype: torch.dtype = torch.float16, device: str = "cuda"):
@@ -238,59 +247,81 @@ class PagedKVCache:
         self.num_layers, self.num_heads, self.head_dim = num_layers, num_heads, head_dim
         self.page_size, self.max_pages, self.dtype, self.device = page_size, max_pages, dtype, device
         self.k_pool = torch.zeros(max_pages, num_heads, page_size, head_dim, dtype=dtype, device=device)
-        self.v_pool = torch.zeros(max_pages, num_heads, page_size, head_dim, dtype=dtype, device=device)
-        self._free_pages = list(range(max_pages))
-        self._used_pages: set = set()
-        self._page_tables: list[list[int]] = [[] for _ in range(num_layers)]
-        self._page_offsets: list[int] = [0] * num_layers
-        self._seq_lens: list[int] = [0] * num_layers
+        self.v_pool = torch.zeros_like(self.k_pool)
+        self._tables = torch.zeros(num_layers, max_pages, dtype=torch.int32, device=device)
+        self._free_pages = list(range(max_pages))  # taken from the end
+        self._used = [False] * max_pages
+        self._n_used = 0
+        self._n_pages = [0] * num_layers  # pages in each layer's table
+        self._seq_lens = [0] * num_layers
+        self._host_tables: list[list[int]] = [[] for _ in range(num_layers)]
+        self._pos = torch.arange(max_pages * page_size, dtype=torch.int64, device=device)
 
+    # ---- page bookkeeping (host)
     def allocate_page(self) -> int:
         if not self._free_pages:
             raise RuntimeError("Page pool exhausted")
         page_id = self._free_pages.pop()
-        self._used_pages.add(page_id)
+        self._used[page_id] = True
+        self._n_used += 1
         return page_id
 
+    def _release(self, page_ids) -> list:
+        """Return used pages to the free list in order; the ids to clear."""
+        freed = []
+        for page_id in page_ids:
+            if 0 <= page_id < self.max_pages and self._used[page_id]:
+                self._used[page_id] = False
+                self._n_used -= 1
+                self._free_pages.append(page_id)
+                freed.append(page_id)
+        return freed
+
+    def _clear(self, page_ids: list):
+        if page_ids:
+            ids = torch.tensor(page_ids, dtype=torch.int64, device=self.device)
+            self.k_pool.index_fill_(0, ids, 0)
+            self.v_pool.index_fill_(0, ids, 0)
+
     def free_page(self, page_id: int):
-        if page_id in self._used_pages:
-            self._used_pages.discard(page_id)
-            self._free_pages.append(page_id)
-            self.k_pool[page_id].zero_()
-            self.v_pool[page_id].zero_()
+        self._clear(self._release([page_id]))
+
+    # ---- data path (device)
+    def _slots(self, layer_idx: int, start: int, n: int):
+        """(page, offset) of the layer's tokens start .. start+n-1, as device index tensors."""
+        pos = self._pos[start:start + n]
+        page = self._tables[layer_idx].index_select(0, pos // self.page_size).long()
+        return page, pos % self.page_size
 
     def append(self, layer_idx: int, keys: torch.Tensor, values: torch.Tensor):
-        """keys / values (heads, N, head_dim): fill the layer's last page, then new ones."""
-        N = keys.shape[1]
-        offset = self._page_offsets[layer_idx]
-        table = self._page_tables[layer_idx]
-        pos = 0
-        while pos < N:
-            if offset == 0 or offset >= self.page_size:
-                table.append(self.allocate_page())
-                offset = 0
-            page_id = table[-1]
-            n = min(self.page_size - offset, N - pos)
-            self.k_pool[page_id, :, offset:offset + n] = keys[:, pos:pos + n]
-            self.v_pool[page_id, :, offset:offset + n] = values[:, pos:pos + n]
-            offset += n
-            pos += n
-        self._page_offsets[layer_idx] = offset
-        self._seq_lens[layer_idx] += N
+        """keys / values (heads, N, head_dim): N tokens after the layer's last one."""
+        N = int(keys.shape[1])
+        if N == 0:
+            return
+        start = self._seq_lens[layer_idx]
+        have = self._n_pages[layer_idx]
+        need = -(-(start + N) // self.page_size)
+        if need > have:
+            new = [self.allocate_page() for _ in range(need - have)]
+            self._host_tables[layer_idx].extend(new)
+            self._tables[layer_idx, have:need] = torch.tensor(new, dtype=torch.int32).to(self.device, non_blocking=True)
+            self._n_pages[layer_idx] = need
+        page, off = self._slots(layer_idx, start, N)
+        self.k_pool[page, :, off] = keys.transpose(0, 1).to(self.dtype)
+        self.v_pool[page, :, off] = values.transpose(0, 1).to(self.dtype)
+        self._seq_lens[layer_idx] = start + N
 
     def get_kv(self, layer_idx: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """The layer's tokens gathered into (heads, seq_len, head_dim) tensors."""
-        seq_len = self._seq_lens[layer_idx]
-        if seq_len == 0:
+        """The layer's tokens as (heads, seq_len, head_dim) tensors."""
+        n = self._seq_lens[layer_idx]
+        if n == 0:
             e = torch.empty(self.num_heads, 0, self.head_dim, dtype=self.dtype, device=self.device)
             return e, e.clone()
-        ids = torch.tensor(self._page_tables[layer_idx], dtype=torch.long, device=self.device)
-        k = self.k_pool[ids].permute(1, 0, 2, 3).reshape(self.num_heads, -1, self.head_dim)
-        v = self.v_pool[ids].permute(1, 0, 2, 3).reshape(self.num_heads, -1, self.head_dim)
-        return k[:, :seq_len], v[:, :seq_len]
+        page, off = self._slots(layer_idx, 0, n)
+        return self.k_pool[page, :, off].transpose(0, 1), self.v_pool[page, :, off].transpose(0, 1)
 
     def get_page_table(self, layer_idx: int) -> torch.Tensor:
-        return torch.tensor(self._page_tables[layer_idx], dtype=torch.int32, device=self.device)
+        return self._tables[layer_idx, :self._n_pages[layer_idx]].clone()
 
     def get_seq_length(self, layer_idx: int) -> int:
         return self._seq_lens[layer_idx]
@@ -301,12 +332,14 @@ class PagedKVCache:
 
     @property
     def memory_usage_mb(self) -> float:
-        return len(self._used_pages) * self.num_heads * self.page_size * self.head_dim * 2 * 2 / 1e6
+        return self._n_used * self.num_heads * self.page_size * self.head_dim * 2 * 2 / 1e6
 
     def reset(self):
-        for table in self._page_tables:
-            for page_id in table:
-                self.free_page(page_id)
-            table.clear()
-        self._page_offsets = [0] * self.num_layers
+        """Free every layer's pages (layer by layer, in table order) and clear them."""
+        freed = []
+        for layer in range(self.num_layers):
+            freed += self._release(self._host_tables[layer])
+            self._host_tables[layer] = []
+        self._clear(freed)
+        self._n_pages = [0] * self.num_layers
         self._seq_lens = [0] * self.num_layers

@@ -443,8 +443,8 @@ def bench_production(args):
 
     def ref_design():
         for lay, (kb, vb) in zip(cache._layers, bufs):
-            kb[:, NW:] = lay._hot_k_contig[:, :NH]
-            vb[:, NW:] = lay._hot_v_contig[:, :NH]
+            kb[:, NW:] = lay.get_hot_kv()[0]
+            vb[:, NW:] = lay.get_hot_kv()[1]
             p = torch.softmax(torch.matmul(kb, qt) * D ** -0.5, dim=1)  # (H, N, 1)
             torch.matmul(p.transpose(1, 2).contiguous(), vb)
 
@@ -468,8 +468,8 @@ def bench_production(args):
         cores = len(os.sched_getaffinity(0))
         lay = cache._layers[0]
         host = [t.cpu().numpy() for a in (lay._warm_k, lay._warm_v) for t in (a.data, a.scales, a.zeros)]
-        hk = lay._hot_k_contig[:, :NH].float().cpu().numpy()
-        hv = lay._hot_v_contig[:, :NH].float().cpu().numpy()
+        hk = lay.get_hot_kv()[0].float().cpu().numpy()
+        hv = lay.get_hot_kv()[1].float().cpu().numpy()
         qn = q[0, :, 0].float().cpu().numpy()
         reps, t_cpu = 0, 0.0
         with threadpool_limits(limits=cores):

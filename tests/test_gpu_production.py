@@ -50,9 +50,26 @@ def test_paged_pool_pages_tables_and_reset():
     assert pc.get_seq_length(0) == 25 and pc.get_seq_length(1) == 17
     assert pc.num_free_pages == 4
     assert pc.memory_usage_mb == pytest.approx(4 * H * 16 * D * 2 * 2 / 1e6)
+    assert pc.get_page_table(0).dtype == torch.int32 and pc.get_page_table(0).device.type == "cuda"
+    # appends that end inside a page, fill it exactly, and cross several pages
+    more = [_rows(rng, H, n, D) for n in (7, 1, 39)]
+    for x in more:
+        pc.append(1, to_dev(x, torch.float16), to_dev(2 * x, torch.float16))
+    full = np.concatenate(a1 + more, axis=1).astype(np.float16)
+    k1, v1 = pc.get_kv(1)
+    bits_equal(k1, full)
+    bits_equal(v1, np.concatenate(a1 + [2 * x for x in more], axis=1).astype(np.float16))
+    assert pc.get_page_table(1).tolist() == [5, 4, 3, 2] and pc.get_seq_length(1) == 64
+    # freeing a page returns it to the end of the free list and zeroes it
+    pc.free_page(2)
+    assert pc.num_free_pages == 3 and float(pc.k_pool[2].abs().sum()) == 0.0 and pc.allocate_page() == 2
     pc.reset()
     assert pc.num_free_pages == 8 and pc.get_seq_length(0) == 0 and pc.get_kv(0)[0].shape == (H, 0, D)
     assert float(pc.k_pool.abs().sum()) == 0.0  # freed pages are zeroed
+    # the reference's free-list order after a reset: layer 0's pages, then layer 1's
+    pc.append(0, to_dev(_rows(rng, H, 1, D), torch.float16), to_dev(_rows(rng, H, 1, D), torch.float16))
+    assert pc.get_page_table(0).tolist() == [2]
+    pc.reset()
     with pytest.raises(RuntimeError, match="exhausted"):
         pc.append(0, torch.zeros(H, 16 * 8 + 1, D, dtype=torch.float16, device="cuda"),
                   torch.zeros(H, 16 * 8 + 1, D, dtype=torch.float16, device="cuda"))
@@ -163,3 +180,29 @@ def test_fused_attention_counter_region_shrinks_then_grows():
     for M in (32, 1, 32, 5, 32):
         q = rng.standard_normal((1, H, M, D)).astype(np.float32)
         assert_close_attn(cache.fused_attention(to_dev(q), 0), orc.attention(q, 0))
+
+
+def test_batched_queries_one_launch_and_hot_accounting():
+    """fused_attention with B = 3 batch elements and M = 2 queries each (one decode launch,
+    rows b * M + m of a head) against the oracle; the hot tier's page accounting follows
+    ceil(hot_len / page_size) pages, and a hot tier past its pages raises."""
+    from akv.production_cache import ProductionCache
+    announce("ProductionCache fused_attention B=3 M=2, hot accounting, exhaustion")
+    cfg = _config(4, 64, num_layers=1, hot_budget=40, warm_budget=128, max_hot_pages=8)
+    cache, orc = ProductionCache(cfg), _oracle(cfg)
+    rng = np.random.default_rng(21)
+    H, D = cfg.num_heads, cfg.head_dim
+    for n in (70, 1, 1, 9):
+        k, v = _rows(rng, H, n, D), _rows(rng, H, n, D)
+        attn = _attn(rng, H, n, cache._layers[0].hot_len + cache._layers[0].warm_len + n)
+        cache.update(to_dev(k[None], torch.float16), to_dev(v[None], torch.float16), 0, to_dev(attn))
+        orc.update(k, v, 0, attn)
+        _check_view(cache, orc, 0, f"append {n}")
+        q = rng.standard_normal((3, H, 2, D)).astype(np.float32)
+        assert_close_attn(cache.fused_attention(to_dev(q), 0), orc.attention(q, 0))
+    lay = cache._layers[0]
+    pages = -(-lay.hot_len // cfg.page_size)
+    assert lay.memory_usage()["hot_mb"] == pytest.approx(pages * H * cfg.page_size * D * 4 / 1e6)
+    with pytest.raises(RuntimeError, match="exhausted"):
+        lay.append_hot(torch.zeros(H, 8 * 16 - lay.hot_len + 1, D, dtype=torch.float16, device="cuda"),
+                       torch.zeros(H, 8 * 16 - lay.hot_len + 1, D, dtype=torch.float16, device="cuda"))
