@@ -303,10 +303,20 @@ def other_workloads(args):
     """The other benchmark configurations, each on its own synthetic inputs, summarised
     (metric, value, roofline, CPU baseline) inside the headline line so one default run
     records every configuration."""
+    import copy
     import torch
     out = {}
+
+    def demote_at(bits):  # the demotion workload at another code width (GPU line only)
+        def run(a):
+            a = copy.copy(a)
+            a.bits, a.no_cpu_baseline = bits, True
+            return bench_demote(a)
+        return run
+
     for name, fn in (("qwen_decode_4k", bench_c1), ("llama7b_decode_16k", bench_decode_mha),
-                     ("llama3_demote_64k", bench_demote), ("llama70b_prefill_128k", bench_prefill),
+                     ("llama3_demote_64k", bench_demote), ("llama3_demote_64k_2bit", demote_at(2)),
+                     ("llama3_demote_64k_4bit", demote_at(4)), ("llama70b_prefill_128k", bench_prefill),
                      ("production_decode_4k", bench_production), ("kivi_decode_4k", bench_kivi)):
         print(f"[bench] workload {name}", file=sys.stderr, flush=True)
         try:
@@ -863,7 +873,8 @@ def bench_demote(args):
                         "frac": round((rd + wr) / (ms_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
                         "traffic": recorded_traffic(s.name) if bits == 3 else None,
                         "kernel": "quant_fast_kernel (gather + quantize + pack, one launch)",
-                        "algorithmic_bytes_per_launch": rd + wr}}
+                        "algorithmic_bytes_per_launch": rd + wr,
+                        "floor_ms_at_peak": round((rd + wr) / (HBM_PEAK_GBPS * 1e9) * 1e3, 4)}}
     if not args.no_cpu_baseline:
         import numpy as np
         cores = len(os.sched_getaffinity(0))

@@ -87,13 +87,15 @@ def _outliers(x: np.ndarray, frac: float, token_axis: int, head_axis: int):
 
 
 def quantize_keys(k: np.ndarray, bits: int, outlier_fraction: float = 0.0,
-                  packed: bool = True, dt=None) -> dict:
-    """akv/affine_quantizer.py:63-110 on k (H, N, D)."""
+                  packed: bool = True, dt=None, outlier_idx=None) -> dict:
+    """akv/affine_quantizer.py:63-110 on k (H, N, D).  ``outlier_idx`` (tests only)
+    imposes the outlier channels instead of ranking them."""
     dt = _dt_of(k, dt)
     k = np.array(k, copy=True)
     res = {}
     if outlier_fraction > 0:
-        idx = _outliers(k, outlier_fraction, token_axis=1, head_axis=0)
+        idx = (_outliers(k, outlier_fraction, token_axis=1, head_axis=0) if outlier_idx is None
+               else np.asarray(outlier_idx, dtype=np.int64))
         res["outlier_idx"] = idx
         res["outlier_data"] = to_dtype(k[..., idx], F16)
         k[..., idx] = 0
@@ -107,13 +109,15 @@ def quantize_keys(k: np.ndarray, bits: int, outlier_fraction: float = 0.0,
 
 
 def quantize_values(v: np.ndarray, bits: int, outlier_fraction: float = 0.0,
-                    packed: bool = True, dt=None) -> dict:
-    """akv/affine_quantizer.py:131-176 on v (H, N, D)."""
+                    packed: bool = True, dt=None, outlier_idx=None) -> dict:
+    """akv/affine_quantizer.py:131-176 on v (H, N, D).  ``outlier_idx`` (tests only)
+    imposes the outlier channels instead of ranking them."""
     dt = _dt_of(v, dt)
     v = np.array(v, copy=True)
     res = {}
     if outlier_fraction > 0:
-        idx = _outliers(v, outlier_fraction, token_axis=1, head_axis=0)
+        idx = (_outliers(v, outlier_fraction, token_axis=1, head_axis=0) if outlier_idx is None
+               else np.asarray(outlier_idx, dtype=np.int64))
         res["outlier_idx"] = idx
         res["outlier_data"] = to_dtype(v[..., idx], F16)
         v[..., idx] = 0
