@@ -206,9 +206,10 @@ class _EventTier:
                 total += x.narrow(2 if name in ("ks", "kz") else 1, 0, self.n_events).nbytes
         return total
 
-    def dequantize_into(self, out_k: torch.Tensor, out_v: torch.Tensor, slots: bool = True):
+    def dequantize_into(self, out_k: torch.Tensor, out_v: Optional[torch.Tensor], slots: bool = True):
         """Dequantize every warm token into out_k / out_v (B, H, rows, D): at its
-        chronological position when ``slots``, else at its warm-tier index."""
+        chronological position when ``slots``, else at its warm-tier index (keys only
+        when ``out_v`` is None)."""
         if self.n == 0:
             return
         t = self.t
@@ -231,7 +232,8 @@ class _EventTier:
         a.B, a.Hkv, a.D = self.B, self.H, self.D
         a.out_dtype = nat.dtype_code(out_k.dtype)
         a.warm = d
-        a.k_out, a.v_out = out_k.data_ptr(), out_v.data_ptr()
+        a.k_out = out_k.data_ptr()
+        a.v_out = out_v.data_ptr() if out_v is not None else None
         a.block_of_token = t["blk"].data_ptr()
         a.n_blocks = self.ecap
         if slots:
@@ -311,15 +313,16 @@ class _HeadBitsTier:
     def resident_bytes(self) -> int:
         return sum(g[2].resident_bytes() for g in self.groups if g[2] is not None)
 
-    def dequantize_into(self, out_k: torch.Tensor, out_v: torch.Tensor, slots: bool = True):
+    def dequantize_into(self, out_k: torch.Tensor, out_v: Optional[torch.Tensor], slots: bool = True):
         rows = out_k.shape[2]
         for bits, heads, tier in self.groups:
             hs = heads.numel()
             tk = torch.empty(self.B * hs, 1, rows, self.D, dtype=out_k.dtype, device=out_k.device)
-            tv = torch.empty_like(tk)
+            tv = torch.empty_like(tk) if out_v is not None else None
             tier.dequantize_into(tk, tv, slots)
             out_k.index_copy_(1, heads, tk.view(self.B, hs, rows, self.D))
-            out_v.index_copy_(1, heads, tv.view(self.B, hs, rows, self.D))
+            if out_v is not None:
+                out_v.index_copy_(1, heads, tv.view(self.B, hs, rows, self.D))
 
     def take(self, idx: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         n = idx.numel()
@@ -430,13 +433,16 @@ class AKVLayer:
                                           torch.ones(n_new, dtype=torch.float32, device=device)])
 
     def _update_proxy_score(self, key_states: torch.Tensor):
-        """akv/drop_in.py:486-525 over the packed tier (its keys dequantized)."""
+        """akv/drop_in.py:486-525 over the packed tier: only its keys are dequantized (one
+        launch, warm-tier order, no copy of the packed arrays)."""
         if self._warm is None or self._warm.n == 0:
             self._proxy_score = None
             return
         probe = key_states.detach().float().mean(dim=(0, 1, 2))
         probe = probe / (probe.norm() + 1e-6)
-        wk, _ = self._warm.take(torch.arange(self._warm.n, device=self._warm.dev))
+        w = self._warm
+        wk = torch.empty(w.B, w.H, w.n, w.D, dtype=torch.float16, device=w.dev)
+        w.dequantize_into(wk, None, slots=False)
         wk_flat = wk.float().mean(dim=(0, 1))
         wk_norm = wk_flat / (wk_flat.norm(dim=-1, keepdim=True) + 1e-6)
         sim = wk_norm @ probe
