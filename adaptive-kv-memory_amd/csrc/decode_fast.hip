@@ -77,20 +77,24 @@ namespace akv {
 // of the merging workgroup), 7 items taken, 8 ticks waiting for ring data, 9 XCC id,
 // 10 first load issued, 11 waves merged in LDS, 12 merger's partial loads done (thread 0),
 // 13 start barrier passed.  Times are s_memrealtime ticks
-// (100 MHz).  The values carry threadIdx.x & 1 (0 on lane 0) so that they live in
-// vector registers and leave through vector stores.
+// (100 MHz).  The words are kept in registers and written once, by lane 0, where the
+// wave leaves the kernel (AKV_TL_FLUSH), so no timeline store waits among the kernel's
+// own memory operations; the values carry threadIdx.x & 1 (0 on lane 0) so that they
+// live in vector registers and leave through vector stores.
 #ifdef AKV_TIMELINE
 constexpr int kTlWords = 16, kTlCap = 1 << 17;
 __device__ unsigned long long g_akv_timeline[kTlCap];
-#define AKV_TL(k, v)                                                                      \
-    do {                                                                                  \
-        if (lane == 0 && tl_base + (k) < kTlCap)                                          \
-            g_akv_timeline[tl_base + (k)] = (unsigned long long)(v) + (threadIdx.x & 1u); \
-    } while (0)
+#define AKV_TL(k, v) (tl_v[(k)] = (unsigned long long)(v) + (threadIdx.x & 1u))
 #define AKV_TL_NOW() __builtin_amdgcn_s_memrealtime()
+#define AKV_TL_FLUSH()                                                        \
+    do {                                                                      \
+        if (lane == 0 && tl_base + kTlWords <= kTlCap)                        \
+            for (int tl_k = 0; tl_k < kTlWords; ++tl_k) g_akv_timeline[tl_base + tl_k] = tl_v[tl_k]; \
+    } while (0)
 #else
 #define AKV_TL(k, v) ((void)0)
 #define AKV_TL_NOW() 0ull
+#define AKV_TL_FLUSH() ((void)0)
 #endif
 
 namespace {
@@ -309,6 +313,9 @@ void decode_fast_kernel(const DecodeParams p) {
     }
 #ifdef AKV_TIMELINE
     const int tl_base = ((int)blockIdx.x * NW + wave) * kTlWords;
+    unsigned long long tl_v[kTlWords];
+#pragma unroll
+    for (int tl_k = 0; tl_k < kTlWords; ++tl_k) tl_v[tl_k] = 0;
     AKV_TL(0, AKV_TL_NOW());
     unsigned long long tl_wait = 0;
     int tl_items = 0;
@@ -1067,7 +1074,10 @@ void decode_fast_kernel(const DecodeParams p) {
             }
         }
     }
-    if (!fused) return;
+    if (!fused) {
+        AKV_TL_FLUSH();
+        return;
+    }
 
     // ---- split merge in the kernel: the workgroup whose partial completes the
     //      (batch, kv-head, row chunk) merges all of them.  The partials were
@@ -1094,13 +1104,19 @@ void decode_fast_kernel(const DecodeParams p) {
     __syncthreads();
     const unsigned role = *work;
     AKV_TL(5, AKV_TL_NOW() * 4ull + role);
-    if (role == 0u) return;
+    if (role == 0u) {
+        AKV_TL_FLUSH();
+        return;
+    }
     // The count returns to zero from the workgroup's last thread when that thread merges
     // nothing (a merging wave would wait for this store with its loads: vmcnt counts stores
     // and loads in issue order).
     if (tid == (nrows * (kD / 4) < 64 * NW ? 64 * NW - 1 : 0))
         __hip_atomic_store(p.split_ctr + bhc, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (tid >= nrows * (kD / 4)) return;
+    if (tid >= nrows * (kD / 4)) {
+        AKV_TL_FLUSH();
+        return;
+    }
     {
         const int rr = tid / (kD / 4), c4 = tid % (kD / 4);
         float M = -INFINITY, L = 0.f;
@@ -1120,6 +1136,7 @@ void decode_fast_kernel(const DecodeParams p) {
             p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
         }
     }
+    AKV_TL_FLUSH();
 }
 
 // LDS slot of the fast kernel: one warm unit, or one 16-token hot K or V half.

@@ -154,14 +154,14 @@ struct KWin {
 // r: the lane's raw code bytes (BK*4 bytes) as little-endian dwords
 template <int BK>
 __device__ __forceinline__ void k_windows(const uint32_t *r, KWin<BK> &W) {
-    if (BK == 3) {
+    if constexpr (BK == 3) {
         W.w[0] = perm(r[1], r[0], 0x04050102u);
         W.w[1] = perm(r[1], r[0], 0x03040001u);
         W.w[2] = perm(r[1], r[0], 0x0C030C00u);
         W.w[3] = perm(r[2], r[1], 0x06070304u);
         W.w[4] = perm(r[2], r[1], 0x05060203u);
         W.w[5] = perm(r[2], r[1], 0x0C050C02u);
-    } else if (BK == 4) {
+    } else if constexpr (BK == 4) {
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
             W.w[2 * d] = r[d];
