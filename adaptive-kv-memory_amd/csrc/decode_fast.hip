@@ -582,9 +582,15 @@ void decode_fast_kernel(const DecodeParams p) {
         {
             // ---- LDS reads at the top of the unit, issued together (the empty asm with a memory
             //      clobber keeps them above it, so their latencies overlap instead of each read
-            //      being waited for before the next is issued): the lane's packed K rows of both
-            //      halves, the V scales of the overflow test, and (block-affine) the lane's K-meta
-            //      pair of the prep below
+            //      being waited for before the next is issued): first (block-affine) the lane's
+            //      K-meta pair of the prep below, then the lane's packed K rows of both halves
+            //      and the V scales of the overflow test.  The prep goes first so that its LDS
+            //      write -> read round trip overlaps the K-window work.
+            h2 s2v = {}, z2v = {};
+            if constexpr (!LEG) {
+                s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
+                z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
+            }
             uint32_t kraw[2][BK];
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
@@ -594,25 +600,7 @@ void decode_fast_kernel(const DecodeParams p) {
             }
             h2 vsv = {};
             if (!LEG && lane * 4 < L::VMB) vsv = as_h2(*(const uint32_t *)(slot + L::VS + 4 * lane));
-            h2 s2v = {}, z2v = {};
-            if constexpr (!LEG) {
-                s2v = lds_h2(slot + L::KS + 2 * kch_lo, slot + L::KS + 2 * kch_hi);
-                z2v = lds_h2(slot + L::KZ + 2 * kch_lo, slot + L::KZ + 2 * kch_hi);
-            }
             asm volatile("" ::: "memory");
-            KWin<BK> W[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) k_windows<BK>(kraw[h], W[h]);
-            // ---- the V fast path holds when no -1024 s of the unit's V scales overflows
-            bool vfast;
-            {
-                bool vfin = true;
-                if (!LEG && lane * 4 < L::VMB) {
-                    const _Float16 n0 = (_Float16)(-1024.0f);
-                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
-                }
-                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
-            }
             // ---- K meta of the block: (s, -2^(10-o) s, z) per channel pair, shared via LDS
             //      and read back per MFMA step; the fast paths hold when no -1024 s overflows
             //      (K and V scales of the unit).  LEG: the lane's 32 channels lie in one group,
@@ -641,6 +629,19 @@ void decode_fast_kernel(const DecodeParams p) {
                 kmw[(1 * 4 + g2) * 16 + pi2] = nb;
                 kmw[(2 * 4 + g2) * 16 + pi2] = as_u32(z2v);
                 __builtin_amdgcn_wave_barrier();
+            }
+            KWin<BK> W[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) k_windows<BK>(kraw[h], W[h]);
+            // ---- the V fast path holds when no -1024 s of the unit's V scales overflows
+            bool vfast;
+            {
+                bool vfin = true;
+                if (!LEG && lane * 4 < L::VMB) {
+                    const _Float16 n0 = (_Float16)(-1024.0f);
+                    vfin = finite2(as_u32(vsv * (h2){n0, n0}));
+                }
+                vfast = !__builtin_amdgcn_ballot_w64(!vfin);
             }
             const u4 *kmr = (const u4 *)kmeta;
 
