@@ -135,9 +135,15 @@ def main():
                          "the same --steps/--warmup and --no-cpu-baseline --calib-copy")
     ap.add_argument("--write-traffic", action="store_true",
                     help="with --summarize-counters: record the HBM bytes per dispatch for the bench line")
+    ap.add_argument("--timeline", choices=["attn", "full"],
+                    help="per-wave phase timestamps of one 32k decode launch (attention only, or with the "
+                         "importance stash) from the timeline build of the library (make -C "
+                         "adaptive-kv-memory_amd/csrc timeline); prints a table, not the bench line")
     args = ap.parse_args()
     if args.summarize_counters:
         return summarize_counters(args.summarize_counters, args.steps, args.warmup, args.write_traffic)
+    if args.timeline:
+        return bench_timeline(args)
     if args.gpus != 1:
         print(json.dumps({"error": "one GPU only: the warm-tier path has no multi-GPU leg (a (batch, kv-head) "
                                    "shard per GPU needs no communication)", "n_gpus": args.gpus}))
@@ -249,6 +255,103 @@ def main():
         torch.neg(src, out=dst)  # one elementwise kernel: reads and writes CALIB_BYTES
         torch.cuda.synchronize()
     print(json.dumps(res), flush=True)
+
+
+# Words of the per-wave timeline the timeline build of the decode kernel records (one
+# launch; times in ticks of the 100 MHz real-time clock): index -> (label, kind).
+_TL_WORDS = [(0, "wave start"), (10, "first load issued"), (13, "start barrier passed"),
+             (1, "first unit landed"), (2, "warm units done"), (3, "last item done"),
+             (11, "12 waves merged in LDS"), (4, "partial written and acknowledged")]
+
+
+def bench_timeline(args):
+    """Per-phase timestamps of one launch of layer 13 of the 32k decode (after the graph
+    of all 28 layers has been timed and replayed): the timeline build records 16 words
+    per wave and writes them where the wave leaves the kernel."""
+    import numpy as np
+    lib_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "adaptive-kv-memory_amd", "akv",
+                            "libakv_hip_timeline.so")
+    if not os.path.exists(lib_path):
+        sys.exit(f"{lib_path} is missing: build it with make -C adaptive-kv-memory_amd/csrc timeline")
+    os.environ["AKV_LIB"] = lib_path
+    import ctypes
+    import torch
+    import akv
+    from akv import _native as nat
+    from akv import workloads as wl
+    from akv.warm_tier import DecodeCall
+    lib = nat.load()
+    words = lib.akv_timeline_words()
+    if words <= 0:
+        sys.exit("the library loaded records no timeline")
+    s = wl.QWEN_DECODE_32K
+    L = args.layers or s.layers
+    calls = []
+    for layer in range(L):
+        k, v = wl.make_kv(s, layer, device="cuda")
+        q = wl.make_q(s, layer, device="cuda")
+        (kw, vw), (kh, vh) = wl.split_hot_warm(k, v, s.n_hot)
+        warm = akv.quantize_kv(kw, vw, s.bits_k, s.bits_v, s.block_t, s.group_v)
+        sc = torch.zeros(s.N, dtype=torch.float32, device="cuda") if args.timeline == "full" else None
+        calls.append(DecodeCall(q, kh, vh, warm, scores=sc, decay=s.decay, hot_first=False))
+        del k, v, kw, vw
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    for _ in range(args.warmup):
+        g.replay()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_layer = e0.elapsed_time(e1) * 1e3 / args.steps / L
+    st = torch.cuda.current_stream().cuda_stream
+    nat.check(lib.akv_timeline_clear(ctypes.c_void_p(st)), "timeline clear")
+    calls[13 % L]()
+    torch.cuda.synchronize()
+    buf = np.zeros(words, dtype=np.uint64)
+    nat.check(lib.akv_timeline_fetch(ctypes.c_void_p(buf.ctypes.data), words), "timeline fetch")
+    t = buf.reshape(-1, 16).astype(np.float64)
+    live = t[:, 0] > 0
+    nw_per_wg = 12  # waves of the kernel's workgroup (no outlier channels)
+    nwg = (int(np.nonzero(live)[0].max()) + 1) // nw_per_wg
+    t = t[: nwg * nw_per_wg]
+    live = t[:, 0] > 0
+    t0 = t[live, 0].min()
+    rel = lambda col: (t[:, col] - t0) / 100.0
+
+    def pct(x):
+        return {"p10": round(float(np.percentile(x, 10)), 2), "p50": round(float(np.median(x)), 2),
+                "p90": round(float(np.percentile(x, 90)), 2), "max": round(float(x.max()), 2)}
+
+    rows = [(label, pct(rel(col)[live])) for col, label in _TL_WORDS]
+    role = t[:, 5].astype(np.uint64) & np.uint64(3)
+    m5 = t[:, 5] > 0
+    t5 = ((t[:, 5].astype(np.uint64) >> np.uint64(2)).astype(np.float64) - t0) / 100.0
+    rows.append(("arrival counted (device-scope atomic)", pct(t5[m5])))
+    m12 = t[:, 12] > 0
+    rows.append(("merging workgroup's partial loads done", pct(rel(12)[m12])))
+    m6 = t[:, 6] > 0
+    rows.append(("merging workgroup done", pct(rel(6)[m6])))
+    t3 = rel(3).reshape(nwg, nw_per_wg)
+    out = {"mode": "timeline", "workload": "qwen_decode_32k", "phase": args.timeline, "layers": L,
+           "graph_us_per_layer": round(us_layer, 3), "workgroups": nwg, "waves": int(live.sum()),
+           "phases_us": {label: v for label, v in rows},
+           "items_per_wave": pct(t[live, 7]), "ticks_waiting_for_ring_data_us": pct(t[live, 8] / 100.0),
+           "workgroup_spread_of_last_item_us": pct(t3.max(1) - t3.min(1)),
+           "merging_workgroups": int((role[m5] != 0).sum()) // nw_per_wg,
+           "items_by_wave_index": [round(float(x), 2) for x in t[:, 7].reshape(nwg, nw_per_wg).mean(0)]}
+    print(f"| phase (us from the launch's first wave) | p10 | p50 | p90 | max |")
+    print("|---|---:|---:|---:|---:|")
+    for label, v in rows:
+        print(f"| {label} | {v['p10']} | {v['p50']} | {v['p90']} | {v['max']} |")
+    print(json.dumps(out), flush=True)
 
 
 def stream_read_reference(nbytes, launches=28, steps=10):
