@@ -1,5 +1,7 @@
 // Dequant / unpack to dense values, device bit-packing, and the importance
 // update from materialised attention weights.
+#include <atomic>
+
 #include "akv_common.h"
 #include "misc.h"
 
@@ -300,11 +302,13 @@ __global__ __launch_bounds__(1024) void select_kernel(const float *scores, int64
     }
 }
 
-// Rows of up to 65536 scores: the same selection with the keys held in
-// registers (element tid + 1024 j in slot j of thread tid), read once.  In the
-// first pass (sign and exponent bits, which cluster) the two most common digits
-// of a wave are added as groups (one LDS atomic each) before the per-lane
-// atomics; the digit searches and the output positions use wave scans (the
+// Rows of up to 65536 scores: the same selection with the keys read once and
+// kept on chip (element tid + 1024 j in slot j of thread tid): slots 0-31 in
+// registers, slots 32-63 in LDS (128 KiB, one 4 KiB row per slot, so a slot's
+// reads are conflict-free) -- all 64 in registers spilled 30 VGPRs to scratch at
+// 1024 threads.  In the first pass (sign and exponent bits, which cluster) the two
+// most common digits of a wave are added as groups (one LDS atomic each) before the
+// per-lane atomics; the digit searches and the output positions use wave scans (the
 // positions from per-(slot, wave) counts scanned in element order).
 __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
 #pragma unroll
@@ -314,31 +318,50 @@ __device__ __forceinline__ uint32_t wave_incl_scan(uint32_t x, int lane) {
     }
     return x;
 }
-constexpr int kSelSlots = 64;
+constexpr int kSelSlots = 64, kSelRegSlots = 32;
+// dynamic LDS of select_reg_kernel: hist[16][256], tot[256], cnt_lt[1024], cnt_eq[1024],
+// s_prefix, s_k (padded to 16 bytes), then the LDS key slots [32][1024]
+constexpr int kSelLdsWords = 16 * 256 + 256 + 2 * 1024 + 4 + (kSelSlots - kSelRegSlots) * 1024;
+constexpr int kSelLdsBytes = kSelLdsWords * 4;
+static_assert(kSelLdsBytes <= 160 * 1024, "select keys exceed the LDS");
 __global__ __launch_bounds__(1024) void select_reg_kernel(const float *scores, int64_t len, int64_t n, int64_t pf,
                                                           int64_t pl, int64_t *out) {
-    __shared__ uint32_t hist[16][256];
-    __shared__ uint32_t tot[256];
-    __shared__ uint32_t cnt_lt[1024], cnt_eq[1024];
-    __shared__ uint32_t s_prefix, s_k;
+    extern __shared__ __align__(16) uint32_t sel_lds[];
+    uint32_t(*hist)[256] = (uint32_t(*)[256])sel_lds;
+    uint32_t *tot = sel_lds + 16 * 256;
+    uint32_t *cnt_lt = tot + 256, *cnt_eq = cnt_lt + 1024;
+    uint32_t &s_prefix = cnt_eq[1024], &s_k = cnt_eq[1025];
+    uint32_t *key_lds = cnt_eq + 1024 + 4;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const float *srow = scores + (int64_t)blockIdx.x * len;
     int64_t *orow = out + (int64_t)blockIdx.x * n;
     const int64_t rec = len - pl > 0 ? len - pl : 0;
-    uint32_t key[kSelSlots];
+    uint32_t key_reg[kSelRegSlots];
     // buffer loads: the slot offset is a constant, so no per-slot address registers
     const __amdgpu_buffer_rsrc_t rs = make_rsrc(srow, (uint32_t)(len * 4));
-#pragma unroll
-    for (int j = 0; j < kSelSlots; ++j)
-        key[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)tid * 4u, 4096 * j, 0);
     // 32-bit position arithmetic against per-thread limits (len <= 65536), so that no
     // per-slot index stays live in a register
     const int lim = (int)len - tid, lim_pf = (int)pf - tid, lim_rec = (int)rec - tid;
-#pragma unroll
-    for (int j = 0; j < kSelSlots; ++j) {
+    auto to_key = [&](int j, uint32_t raw) {
         const bool prot = 1024 * j < lim_pf || 1024 * j >= lim_rec;
-        key[j] = 1024 * j < lim ? (prot ? kKeyInf : order_key(__builtin_bit_cast(float, key[j]))) : 0u;
+        return 1024 * j < lim ? (prot ? kKeyInf : order_key(__builtin_bit_cast(float, raw))) : 0u;
+    };
+#pragma unroll
+    for (int j = 0; j < kSelRegSlots; ++j)
+        key_reg[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)tid * 4u, 4096 * j, 0);
+#pragma unroll
+    for (int j0 = kSelRegSlots; j0 < kSelSlots; j0 += 8) {  // LDS slots, 8 loads in flight at a time
+        uint32_t raw[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) raw[i] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)tid * 4u, 4096 * (j0 + i), 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) key_lds[(j0 + i - kSelRegSlots) * 1024 + tid] = to_key(j0 + i, raw[i]);
     }
+#pragma unroll
+    for (int j = 0; j < kSelRegSlots; ++j) key_reg[j] = to_key(j, key_reg[j]);
+    // slot j of this thread (j a compile-time constant after unrolling); a thread reads
+    // only its own LDS slots, so they need no barrier
+    auto key = [&](int j) -> uint32_t { return j < kSelRegSlots ? key_reg[j] : key_lds[(j - kSelRegSlots) * 1024 + tid]; };
     auto valid = [&](int j) { return 1024 * j < lim; };
     if (tid == 0) {
         s_prefix = 0u;
@@ -352,8 +375,8 @@ __global__ __launch_bounds__(1024) void select_reg_kernel(const float *scores, i
         const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
 #pragma unroll
         for (int j = 0; j < kSelSlots; ++j) {
-            const uint32_t d = (key[j] >> shift) & 255u;
-            bool pend = valid(j) && (key[j] & hmask) == prefix;
+            const uint32_t d = (key(j) >> shift) & 255u;
+            bool pend = valid(j) && (key(j) & hmask) == prefix;
             if (pass == 0) {  // the sign / exponent digit clusters: add the two most common
                               // digits of the wave as groups, the rest per lane
 #pragma unroll
@@ -396,8 +419,8 @@ __global__ __launch_bounds__(1024) void select_reg_kernel(const float *scores, i
     // counts of (slot j, wave w) at entry 16 j + w: element order
 #pragma unroll
     for (int j = 0; j < kSelSlots; ++j) {
-        const uint64_t ml = __builtin_amdgcn_ballot_w64(valid(j) && key[j] < tau);
-        const uint64_t me = __builtin_amdgcn_ballot_w64(valid(j) && key[j] == tau);
+        const uint64_t ml = __builtin_amdgcn_ballot_w64(valid(j) && key(j) < tau);
+        const uint64_t me = __builtin_amdgcn_ballot_w64(valid(j) && key(j) == tau);
         if (lane == 0) {
             cnt_lt[16 * j + wave] = (uint32_t)__builtin_popcountll(ml);
             cnt_eq[16 * j + wave] = (uint32_t)__builtin_popcountll(me);
@@ -423,7 +446,7 @@ __global__ __launch_bounds__(1024) void select_reg_kernel(const float *scores, i
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < kSelSlots; ++j) {
-        const bool lt = valid(j) && key[j] < tau, eq = valid(j) && key[j] == tau;
+        const bool lt = valid(j) && key(j) < tau, eq = valid(j) && key(j) == tau;
         const uint64_t ml = __builtin_amdgcn_ballot_w64(lt), me = __builtin_amdgcn_ballot_w64(eq);
         const uint32_t lt_before = cnt_lt[16 * j + wave] + __builtin_amdgcn_mbcnt_hi((uint32_t)(ml >> 32),
                                        __builtin_amdgcn_mbcnt_lo((uint32_t)ml, 0u));
@@ -439,8 +462,23 @@ __global__ __launch_bounds__(1024) void select_reg_kernel(const float *scores, i
 hipError_t select_launch(const float *scores, int64_t rows, int64_t len, int64_t n, int64_t pf, int64_t pl,
                          int64_t *out, hipStream_t s) {
     if (rows <= 0 || n <= 0) return hipSuccess;
-    if (len <= 1024 * kSelSlots)
-        hipLaunchKernelGGL(select_reg_kernel, dim3((unsigned)rows), dim3(1024), 0, s, scores, len, n, pf, pl, out);
+    if (len <= 1024 * kSelSlots) {
+        // raise the dynamic LDS cap above 64 KiB once per device (a bit per device index;
+        // host threads that race here both set it, which is harmless)
+        static std::atomic<uint64_t> attr_devs{0};
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        const uint64_t bit = (dev >= 0 && dev < 64) ? 1ull << dev : 0ull;
+        if (!bit || !(attr_devs.load(std::memory_order_acquire) & bit)) {
+            e = hipFuncSetAttribute((const void *)select_reg_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    kSelLdsBytes);
+            if (e != hipSuccess) return e;
+            attr_devs.fetch_or(bit, std::memory_order_release);
+        }
+        hipLaunchKernelGGL(select_reg_kernel, dim3((unsigned)rows), dim3(1024), kSelLdsBytes, s, scores, len, n, pf,
+                           pl, out);
+    }
     else
         hipLaunchKernelGGL(select_kernel, dim3((unsigned)rows), dim3(1024), 0, s, scores, len, n, pf, pl, out);
     return hipGetLastError();
