@@ -151,13 +151,15 @@ __device__ __forceinline__ h4 softmax_tile(WaveState &st, f4 s, float sl2) {
     return (h4){(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
 }
 
+// The stash holds the raw logits q.k; its readers take them to the log2 domain with
+// the softmax's own fma, 2^(x sl2 - M) (one rounding).
 __device__ __forceinline__ void store_stash(const DecodeParams &p, int64_t rowbase, int row_valid, int64_t nlog0,
-                                            f4 s, float sl2, int nvalid) {
+                                            f4 s, int nvalid) {
     if (!p.stash || !row_valid) return;
     float *dst = p.stash + rowbase + nlog0;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (i < nvalid) dst[i] = s[i] * sl2;
+        if (i < nvalid) dst[i] = s[i];
 }
 
 // raw loads of one warm tile
@@ -346,7 +348,7 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
                 for (int i = 0; i < 4; ++i)
                     if (i >= nvalid) s[i] = -INFINITY;
             }
-            store_stash(p, strow, row_valid, seg_base + t0 + 4 * grp, s, sl2, nvalid);
+            store_stash(p, strow, row_valid, seg_base + t0 + 4 * grp, s, nvalid);
             const h4 pop = softmax_tile(stt, s, sl2);
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -572,7 +574,7 @@ __global__ __launch_bounds__(256) AKV_SPLIT_ATTR void decode_split_kernel(const 
                         }
                     }
                 }
-                store_stash(p, strow, row_valid, seg_base + t0 + 4 * grp, s, sl2, nvalid);
+                store_stash(p, strow, row_valid, seg_base + t0 + 4 * grp, s, nvalid);
 
                 const h4 pop = softmax_tile(stt, s, sl2);
                 // ---- V dequant (4 tokens x 8 channels of chunk col) + PV per channel slot
@@ -848,12 +850,13 @@ __global__ __launch_bounds__(256) void decode_reduce_kernel(const DecodeParams p
     merge_split_row<D>(p, blockIdx.x, blockIdx.y, sm, sls, accl);
 }
 
-// Normalise the stashed log2-domain logits into attention weights and/or
+// Normalise the stashed logits into attention weights, 2^(x sl2 - M) / L, and/or
 // accumulate the importance EMA.  Workgroup = 64 tokens x 16 row lanes: thread
 // (token t, row lane rl) walks rows rl, rl+16, ... for tokens t, t+16, t+32,
 // t+48; the row lanes are summed through LDS.
 __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodeParams p) {
     __shared__ float red[16][65];
+    const float sl2 = p.scale_log2;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M;
     const int t = threadIdx.x & 15, rl = threadIdx.x >> 4;
     const int64_t n0 = (int64_t)blockIdx.x * 64 + t;
@@ -867,7 +870,7 @@ __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodePar
         for (int i = 0; i < 4; ++i) x[i] = (n0 + 16 * i < N) ? srow[n0 + 16 * i] : -INFINITY;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[i] - M);
+            const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], sl2, -M));
             const float wgt = e * inv;
             if (p.attn_out && n0 + 16 * i < N) srow[n0 + 16 * i] = wgt;
             imp[i] += (n0 + 16 * i < N) ? wgt : 0.f;
@@ -910,6 +913,7 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
     __shared__ float red[NRL][TPW + 1];
     const int tid = threadIdx.x, q = tid % NQ, rl = tid / NQ;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M, N = p.N;
+    const float sl2 = p.scale_log2;
     const int64_t n0 = (int64_t)blockIdx.x * TPW + 4 * q;
     // the old score is loaded with the first batch of logits, not after the reduction
     const int64_t ns = (int64_t)blockIdx.x * TPW + tid;
@@ -944,7 +948,7 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
             f4 w;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float e = (M[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[j][i] - M[j]);
+                const float e = (M[j] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(x[j][i], sl2, -M[j]));
                 w[i] = e * W[j];
                 if (n0 + i < N) imp[i] += w[i];
             }
@@ -996,6 +1000,7 @@ __global__ __launch_bounds__(256) void finish_kernel(const DecodeParams p) {
     const int tid = threadIdx.x;
     const int rows = p.B * p.Hq * p.M;
     const int ns = p.nsplit;
+    const float sl2 = p.scale_log2;
     const int64_t PS = D + 4;
     const int64_t pstride = (int64_t)p.prows * PS;
 
@@ -1063,7 +1068,7 @@ __global__ __launch_bounds__(256) void finish_kernel(const DecodeParams p) {
             const float M = rM[r], W = rW[r];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x[j][i] - M);
+                const float e = (M == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(x[j][i], sl2, -M));
                 const float wgt = e * W;
                 if (n0 + 16 * i < N) {
                     if (p.attn_out) p.stash[(int64_t)r * N + n0 + 16 * i] = wgt;

@@ -211,23 +211,23 @@ __device__ __forceinline__ void issue_hot(u4 r, unsigned char *slot, int lane, i
     dma_lean<4096>(r, lds_addr(slot), (uint32_t)tile * 4096u, (uint32_t)lane * 16u, (uint32_t)lane * 4u);
 }
 
-// Logits of 4 consecutive tokens of one row (log2 domain): one 16-byte store when
-// all 4 are valid and the row offset is 16-byte aligned (vec), else one per token.
-// The 16-byte stores write through to the device coherence point (cache policy
-// sc1): the stash leaves during the kernel instead of in the end-of-kernel L2
-// write-back (measured 0.35 us per layer faster at the 32k workload).
+// Raw logits q.k of 4 consecutive tokens of one row (the weights kernels take them to
+// the log2 domain): one 16-byte store when all 4 are valid and the row offset is
+// 16-byte aligned (vec), else one per token.  The 16-byte stores write through to the
+// device coherence point (cache policy sc1): the stash leaves during the kernel instead
+// of in the end-of-kernel L2 write-back (measured 0.35 us per layer faster at the 32k
+// workload).  Whole warm units take a cheaper path in the loop itself.
 __device__ __forceinline__ void stash4(const DecodeParams &p, int64_t strow, int row_valid, int64_t n0, f4 s,
-                                       float sl2, int nvalid, bool vec, __amdgpu_buffer_rsrc_t srs, int64_t sbase) {
+                                       int nvalid, bool vec, __amdgpu_buffer_rsrc_t srs, int64_t sbase) {
     if (!p.stash || !row_valid) return;
     float *dst = p.stash + strow + n0;
     if (vec && nvalid >= 4) {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, s * sl2), srs, (int)((strow + n0 - sbase) * 4),
-                                               0, 16);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, s), srs, (int)((strow + n0 - sbase) * 4), 0, 16);
         return;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        if (i < nvalid) dst[i] = s[i] * sl2;
+        if (i < nvalid) dst[i] = s[i];
 }
 
 // Online merge of the nsplit partials (m, l, acc) of row rr, channels 4 c4 .. +3,
@@ -362,6 +362,9 @@ void decode_fast_kernel(const DecodeParams p) {
         make_rsrc(p.stash ? p.stash + sbase : p.stash, st_buf_ok ? (uint32_t)(p.R * p.N * 4) : 0u);
     const bool st_vec_w = st_buf_ok && p.N % 4 == 0 && warm_base % 4 == 0,
                st_vec_h = st_buf_ok && p.N % 4 == 0 && hot_base % 4 == 0;
+    // byte offset of the lane's 4 logits of warm token 0 within those rows (a whole unit's
+    // stores add its token offset as the scalar operand)
+    const uint32_t st_w_voff = st_vec_w ? (uint32_t)((strow - sbase + warm_base + 4 * grp) * 4) : 0u;
 
     // this workgroup's items: warm 32-token units, then hot 16-token tiles (the
     // cheap hot items come last and even out the waves' finishing times)
@@ -796,10 +799,20 @@ void decode_fast_kernel(const DecodeParams p) {
                 }
             }
             if (p.stash) {
+                if (st_vec_w && tok0 + kUnit <= nw) {  // a whole unit: two 16-byte stores per lane
+                    if (row_valid) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int t0 = tok0 + 16 * h;
-                    stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], sl2, min(4, nw - (t0 + 4 * grp)), st_vec_w, srs, sbase);
+                        for (int h = 0; h < 2; ++h)
+                            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, sc[h]), srs, (int)st_w_voff,
+                                                                   (tok0 + 16 * h) * 4, 16);
+                    }
+                } else {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int t0 = tok0 + 16 * h;
+                        stash4(p, strow, row_valid, warm_base + t0 + 4 * grp, sc[h], min(4, nw - (t0 + 4 * grp)),
+                               st_vec_w, srs, sbase);
+                    }
                 }
             }
             const h8 pop = softmax32(stt, sc[0], sc[1], sl2);
@@ -991,7 +1004,7 @@ void decode_fast_kernel(const DecodeParams p) {
                 for (int ii = 0; ii < 4; ++ii)
                     if (ii >= nvalid) sh[ii] = -INFINITY;
             }
-            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, sl2, nvalid, st_vec_h, srs, sbase);
+            stash4(p, strow, row_valid, hot_base + t0 + 4 * grp, sh, nvalid, st_vec_h, srs, sbase);
             hot_p = softmax16(stt, sh, sl2);
         } else {
             // ---- hot V tile: lane = (chunk col, tokens 4 grp .. +3)
