@@ -13,7 +13,7 @@ from typing import Optional
 
 import torch
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 AKV_OK = 0
 AKV_E_INVALID = -1
@@ -83,6 +83,7 @@ class PrefillArgs(ctypes.Structure):
         ("warm", WarmDesc),
         ("out", _vp),
         ("workspace", _vp), ("workspace_bytes", _i64),
+        ("k_chunk", _vp), ("v_chunk", _vp),
     ]
 
 

@@ -253,19 +253,32 @@ def decode_attention(q: torch.Tensor, k_hot: Optional[torch.Tensor], v_hot: Opti
 
 def prefill_attention(q: torch.Tensor, k_hot: Optional[torch.Tensor], v_hot: Optional[torch.Tensor],
                       warm: Optional[WarmTier], sm_scale: Optional[float] = None,
-                      num_splits: int = 0) -> torch.Tensor:
+                      num_splits: int = 0, k_chunk: Optional[torch.Tensor] = None,
+                      v_chunk: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Chunked-prefill attention: q (B, Hq, M, D) fp16 or bf16 -- M positions
     after every cached token, so no mask over the cache -- over hot fp16
     (B, Hkv, Nh, D) and the packed warm tier; returns (B, Hq, M, D) in q's
-    dtype.  No attention weights (the M x N matrix is never formed)."""
+    dtype.  No attention weights (the M x N matrix is never formed).
+
+    ``k_chunk`` / ``v_chunk`` (B, Hkv, M, D) in q's dtype are the chunk's own keys
+    and values: with them every position m also attends to chunk tokens 0..m
+    (causal self-attention of the chunk, after the cache)."""
     lib = nat.load()
-    nat.require_device(q, k_hot, v_hot)
+    nat.require_device(q, k_hot, v_hot, k_chunk, v_chunk)
     if q.dtype not in (torch.float16, torch.bfloat16):
         raise TypeError("prefill takes float16 or bfloat16 queries")
     q = nat.dev_contig(q)
     B, Hq, M, D = q.shape
     k_hot, v_hot, n_hot = _hot_ptrs(k_hot, v_hot, q.new_empty(0, dtype=torch.float16))
-    Hkv = warm.heads if warm is not None else k_hot.shape[1]
+    Hkv = warm.heads if warm is not None else (k_hot.shape[1] if n_hot else
+                                               (k_chunk.shape[1] if k_chunk is not None else 0))
+    if (k_chunk is None) != (v_chunk is None):
+        raise ValueError("k_chunk and v_chunk go together")
+    if k_chunk is not None:
+        for t in (k_chunk, v_chunk):
+            if t.dtype != q.dtype or tuple(t.shape) != (B, Hkv, M, D):
+                raise ValueError(f"k_chunk / v_chunk must be ({B}, {Hkv}, {M}, {D}) in {q.dtype}")
+        k_chunk, v_chunk = nat.dev_contig(k_chunk), nat.dev_contig(v_chunk)
     out = torch.empty_like(q)
     a = nat.PrefillArgs()
     a.abi_version = nat.ABI_VERSION
@@ -282,6 +295,8 @@ def prefill_attention(q: torch.Tensor, k_hot: Optional[torch.Tensor], v_hot: Opt
         a.warm.kind = nat.WARM_NONE
     a.out = out.data_ptr()
     a.num_splits = int(num_splits)
+    if k_chunk is not None:
+        a.k_chunk, a.v_chunk = k_chunk.data_ptr(), v_chunk.data_ptr()
     nbytes = lib.akv_prefill_workspace_bytes(ctypes.byref(a))
     if nbytes < 0:
         nat.check(lib.akv_prefill_attn(ctypes.byref(a), None), "prefill_attention")

@@ -232,7 +232,10 @@ int check_prefill(const akv_prefill_args *a) {
     const akv_warm_desc &w = a->warm;
     const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
     if (nw < 0) return fail(AKV_E_SHAPE, "n_warm < 0");
-    if (a->n_hot + nw < 1) return fail(AKV_E_SHAPE, "no tokens to attend to");
+    if (!a->k_chunk != !a->v_chunk) return fail(AKV_E_INVALID, "k_chunk and v_chunk go together");
+    if (a->k_chunk && (!aligned16(a->k_chunk) || !aligned16(a->v_chunk)))
+        return fail(AKV_E_ALIGN, "k_chunk/v_chunk must be 16-byte aligned");
+    if (a->n_hot + nw < 1 && !a->k_chunk) return fail(AKV_E_SHAPE, "no tokens to attend to");
     if (!a->q || !a->out) return fail(AKV_E_INVALID, "q and out are required");
     if (!aligned16(a->q) || !aligned16(a->out)) return fail(AKV_E_ALIGN, "q/out must be 16-byte aligned");
     if (a->n_hot > 0) {
@@ -271,7 +274,7 @@ void make_prefill_plan(const akv_prefill_args *a, PrefillPlan *pl) {
     pl->R = g * a->M;
     pl->n_row_tiles = (pl->R + akv::kPrefillRows - 1) / akv::kPrefillRows;
     const int64_t nw = a->warm.kind == AKV_WARM_NONE ? 0 : a->warm.n_warm;
-    const int64_t nt = (a->n_hot + 31) / 32 + (nw + 31) / 32;
+    const int64_t nt = (a->n_hot + 31) / 32 + (nw + 31) / 32 + (a->k_chunk ? (a->M + 31) / 32 : 0);
     const int64_t wgs = (int64_t)a->B * a->Hkv * pl->n_row_tiles;
     int64_t ns = a->num_splits > 0 ? a->num_splits : (kCUs + wgs - 1) / wgs;
     if (a->num_splits <= 0 && ns > nt / 8) ns = nt / 8;
@@ -693,6 +696,8 @@ int akv_prefill_attn(const akv_prefill_args *a, void *stream) {
     p.tiles_per_split = pl.tiles_per_split;
     p.part = (float *)a->workspace;
     p.nchunk = pl.nchunk; p.prows = pl.prows;
+    p.kcur = a->k_chunk; p.vcur = a->v_chunk;
+    p.n_cur = a->k_chunk ? a->M : 0;
     hipError_t e = akv::prefill_launch(p, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "prefill launch");
     return ok();

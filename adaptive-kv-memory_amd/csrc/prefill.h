@@ -23,6 +23,8 @@ struct PrefillParams {
     int64_t tiles_per_split;        // 32-token tiles per split (hot tiles first, then warm)
     float *part;                    // partials, decode layout (16-row chunks), when nsplit > 1
     int nchunk, prows;              // 16-row chunks of R and rows per partial (decode layout)
+    const void *kcur, *vcur;        // the chunk's own K / V [B][Hkv][M][128] in q's dtype (or null):
+    int n_cur;                      // attended causally after the cache; n_cur = M (0 without them)
 };
 
 constexpr int kPrefillRows = 256;   // query rows per workgroup

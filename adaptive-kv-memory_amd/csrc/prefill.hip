@@ -7,8 +7,9 @@
 // share every dequantized tile.  Wave w owns rows 32w .. 32w+31 as two
 // 16-row MFMA column groups.
 //
-// The cache is walked in 32-token tiles (hot tiles, then warm units), double
-// buffered in LDS.  While the MFMAs consume tile j, waves 0-3 dequantize tile
+// The cache is walked in 32-token tiles (hot tiles, then warm units, then --
+// when the chunk's own K/V are given -- the chunk's tokens under a causal mask:
+// query position m sees chunk tokens 0..m), double buffered in LDS.  While the MFMAs consume tile j, waves 0-3 dequantize tile
 // j+1's K and waves 4-7 its V from registers loaded one tile ahead:
 //   K tile  [32 tokens][4 channel groups][16 code pairs] u32, pair order of
 //           kpair_chan() (the query operand is permuted to match), exact
@@ -57,7 +58,9 @@ __device__ __forceinline__ uint32_t bf16x2_to_h2(uint32_t w) {
 
 }  // namespace
 
-template <int BK, int BV, int NG>
+// OWN: the chunk's own keys / values follow the cache (a variant of its own, so that the
+// cache loop of the plain kernel keeps its registers)
+template <int BK, int BV, int NG, bool OWN>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(const PrefillParams p) {
     constexpr int KR = 16 * BK, VR = 16 * BV, GV = kPD / NG;
@@ -77,9 +80,10 @@ void prefill_kernel(const PrefillParams p) {
     const int64_t bh = (int64_t)b * p.Hkv + kvh;
     const int r0 = rtile * kPrefillRows;
 
-    // ---- token tiles of this split: hot tiles first, then warm units
+    // ---- token tiles of this split: hot tiles first, then warm units, then the chunk's own
     const int n_ht = (int)((p.n_hot + kPTok - 1) / kPTok), n_wt = (int)((p.n_warm + kPTok - 1) / kPTok);
-    const int nt = n_ht + n_wt;
+    const int c_first = n_ht + n_wt;  // first tile of the chunk's own tokens
+    const int nt = c_first + (OWN ? (p.n_cur + kPTok - 1) / kPTok : 0);
     const int t_begin = (int)min((int64_t)split * p.tiles_per_split, (int64_t)nt);
     const int t_end = (int)min((int64_t)t_begin + p.tiles_per_split, (int64_t)nt);
     const int n_hot32 = (int)p.n_hot, n_warm32 = (int)p.n_warm;
@@ -110,10 +114,14 @@ void prefill_kernel(const PrefillParams p) {
             qop[rg][st] = __builtin_bit_cast(h8, (u4){pairs[4 * st], pairs[4 * st + 1], pairs[4 * st + 2], pairs[4 * st + 3]});
     }
 
+    // With the chunk's own tokens a split that begins past the chunk's first tile can hold
+    // no token a row sees (all masked): a finite start for the running max keeps such a
+    // row's bias finite, so its probabilities are exp2(-inf) = 0 and its partial is
+    // (max -2^126, sum 0), which the merge weights by exp2(-2^126 - max) = 0.
     Soft sm[2];
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
-        sm[rg].m2 = -INFINITY;
+        sm[rg].m2 = OWN ? -0x1p126f : -INFINITY;
         sm[rg].l = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; ++j) sm[rg].acc[j] = (f4){0.f, 0.f, 0.f, 0.f};
@@ -335,16 +343,17 @@ void prefill_kernel(const PrefillParams p) {
         }
     };
 
-    // ---- the tile loop: load t+1 | MFMA on t | dequant t+1 | barrier
-    if (t_begin < t_end) {
+    // ---- the tile loop over the cache: load t+1 | MFMA on t | dequant t+1 | barrier
+    const int tc_end = t_end < c_first ? t_end : c_first;
+    if (t_begin < tc_end) {
         load_tile(t_begin);
         stage_tile(t_begin, smem);
     }
     __syncthreads();
-    for (int t = t_begin; t < t_end; ++t) {
+    for (int t = t_begin; t < tc_end; ++t) {
         const int cur = (int)((t - t_begin) & 1);
         unsigned char *buf = smem + cur * kBuf;
-        const bool more = t + 1 < t_end;
+        const bool more = t + 1 < tc_end;
         if (more) load_tile(t + 1);
 
         const bool hot = t < n_ht;
@@ -402,6 +411,118 @@ void prefill_kernel(const PrefillParams p) {
         __syncthreads();
     }
 
+    // ---- the chunk's own tiles (when given and in this split): token rows in q's dtype,
+    //      read like the hot tier's (bf16 converted to fp16, exact in fp16's range, as the
+    //      queries are), a causal mask, no zero-points.  A loop of its own, so that its
+    //      descriptors and row positions are live only here.
+    const int tq_begin = t_begin > c_first ? t_begin : c_first;
+    if (OWN && tq_begin < t_end) {
+        const __amdgpu_buffer_rsrc_t rkq =
+            make_rsrc((const uint16_t *)p.kcur + bh * p.n_cur * kPD, (uint32_t)(p.n_cur * kPD * 2));
+        const __amdgpu_buffer_rsrc_t rvq =
+            make_rsrc((const uint16_t *)p.vcur + bh * p.n_cur * kPD, (uint32_t)(p.n_cur * kPD * 2));
+        int mrow[2];  // chunk position of each column group's row
+#pragma unroll
+        for (int rg = 0; rg < 2; ++rg) {
+            const int r = r0 + 32 * wave + 16 * rg + col;
+            mrow[rg] = (r < p.R ? r : r0) % p.M;
+        }
+        auto load_own = [&](int t) {
+            const uint32_t tok0 = (uint32_t)(t - c_first) * kPTok;
+            if (kwave) {
+                const uint32_t off = ((tok0 + ktok) * kPD + 32 * grp) * 2u;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hraw[i] = bld128(rkq, off + 16u * i);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    hraw[i] = bld128(rvq, ((tok0 + 16 * vh + 4 * grp + 2 * vp + i) * kPD + 8 * col) * 2u);
+            }
+        };
+        auto stage_own = [&](unsigned char *buf) {
+            unsigned char *kt = buf, *vt = buf + kKTile;
+            if (kwave) {
+                uint32_t nat[16], pairs[16];
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) nat[4 * q4 + e] = p.q_bf16 ? bf16x2_to_h2(hraw[q4][e]) : hraw[q4][e];
+                hot_k_pairs<BK>(nat, pairs);
+                u4 *dst = (u4 *)(kt + ktok * kKRow + grp * 64 + kph * 32);
+                if (kph == 0) {
+                    dst[0] = (u4){pairs[0], pairs[1], pairs[2], pairs[3]};
+                    dst[1] = (u4){pairs[4], pairs[5], pairs[6], pairs[7]};
+                } else {
+                    dst[0] = (u4){pairs[8], pairs[9], pairs[10], pairs[11]};
+                    dst[1] = (u4){pairs[12], pairs[13], pairs[14], pairs[15]};
+                }
+            } else {
+                u4 w2[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) w2[i][e] = p.q_bf16 ? bf16x2_to_h2(hraw[i][e]) : hraw[i][e];
+#pragma unroll
+                for (int kk = 0; kk < 8; ++kk) {
+                    const uint32_t sel = (kk & 1) ? 0x07060302u : 0x05040100u;
+                    *(uint32_t *)(vt + (((kk * 2 + vh) * 2 + vp) * 64 + lane) * 4) = perm(w2[1][kk / 2], w2[0][kk / 2], sel);
+                }
+            }
+        };
+        load_own(tq_begin);
+        stage_own(smem);
+        __syncthreads();
+        for (int t = tq_begin; t < t_end; ++t) {
+            const int cur = (int)((t - tq_begin) & 1);
+            const unsigned char *buf = smem + cur * kBuf;
+            const bool more = t + 1 < t_end;
+            if (more) load_own(t + 1);
+            const int tok0 = (t - c_first) * kPTok;
+            const unsigned char *kt = buf, *vt = buf + kKTile;
+            f4 sc[2][2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                sc[0][h] = (f4){0.f, 0.f, 0.f, 0.f};
+                sc[1][h] = (f4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const h8 a = *(const h8 *)(kt + (16 * h + col) * kKRow + grp * 64 + 16 * st);
+                    sc[0][h] = mfma_k32(a, qop[0][st], sc[0][h]);
+                    sc[1][h] = mfma_k32(a, qop[1][st], sc[1][h]);
+                }
+            }
+            // causal: position m sees chunk tokens 0..m (so none past the chunk's end)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = tok0 + 16 * h + 4 * grp + i;
+                    if (j > mrow[0]) sc[0][h][i] = -INFINITY;
+                    if (j > mrow[1]) sc[1][h][i] = -INFINITY;
+                }
+            h8 pop[2];
+            pop[0] = softmax32(sm[0], sc[0][0], sc[0][1], sl2);
+            pop[1] = softmax32(sm[1], sc[1][0], sc[1][1], sl2);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) {
+                const uint32_t *va = (const uint32_t *)(vt + (kk * 4 * 64 + lane) * 4);
+                const h8 a = __builtin_bit_cast(h8, (u4){va[0], va[64], va[128], va[192]});
+                sm[0].acc[kk] = mfma_k32(a, pop[0], sm[0].acc[kk]);
+                sm[1].acc[kk] = mfma_k32(a, pop[1], sm[1].acc[kk]);
+            }
+            {
+                // the row sums of P (chunk row 15 takes ones; no zero-points here)
+                const u4 zw = col == 15 ? (u4){0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u}
+                                        : (u4){0u, 0u, 0u, 0u};
+                const h8 az = __builtin_bit_cast(h8, zw);
+                sm[0].accz = mfma_k32(az, pop[0], sm[0].accz);
+                sm[1].accz = mfma_k32(az, pop[1], sm[1].accz);
+            }
+            if (more) stage_own(smem + (cur ^ 1) * kBuf);
+            __syncthreads();
+        }
+    }
+
     // ---- output (one split) or partials (decode split layout)
 #pragma unroll
     for (int rg = 0; rg < 2; ++rg) {
@@ -455,7 +576,10 @@ int prefill_lds_bytes() { return kPLds; }
 template <int BK, int BV, int NG>
 static hipError_t launch_prefill(const PrefillParams &p, hipStream_t s) {
     const unsigned nwg = (unsigned)(p.B * p.Hkv * p.nsplit * p.n_row_tiles);
-    hipLaunchKernelGGL((prefill_kernel<BK, BV, NG>), dim3(nwg), dim3(kPThreads), kPLds, s, p);
+    if (p.kcur && p.n_cur > 0)
+        hipLaunchKernelGGL((prefill_kernel<BK, BV, NG, true>), dim3(nwg), dim3(kPThreads), kPLds, s, p);
+    else
+        hipLaunchKernelGGL((prefill_kernel<BK, BV, NG, false>), dim3(nwg), dim3(kPThreads), kPLds, s, p);
     return hipGetLastError();
 }
 

@@ -123,8 +123,9 @@ def main():
     ap.add_argument("--calib-copy", action="store_true",
                     help="end with one device copy of 256 MiB (reference dispatch for counter runs)")
     ap.add_argument("--workload", default="qwen_decode_32k",
-                    choices=["qwen_decode_32k", "llama7b_decode_16k", "llama70b_prefill_128k", "llama3_demote_64k",
-                             "qwen_decode_4k", "production_decode_4k", "kivi_decode_4k"],
+                    choices=["qwen_decode_32k", "llama7b_decode_16k", "llama70b_prefill_128k",
+                             "llama70b_prefill_128k_causal", "llama3_demote_64k", "qwen_decode_4k",
+                             "production_decode_4k", "kivi_decode_4k"],
                     help="the headline decode step (default; the other workloads are summarised in its "
                          "'workloads' field), or one other workload on its own line")
     ap.add_argument("--no-other-workloads", action="store_true",
@@ -155,6 +156,7 @@ def main():
     from akv.warm_tier import DecodeCall
     if args.workload != "qwen_decode_32k":
         fn = {"llama70b_prefill_128k": bench_prefill, "llama3_demote_64k": bench_demote,
+              "llama70b_prefill_128k_causal": lambda a: bench_prefill(a, causal=True),
               "llama7b_decode_16k": bench_decode_mha, "qwen_decode_4k": bench_c1,
               "production_decode_4k": bench_production, "kivi_decode_4k": bench_kivi}[args.workload]
         print(json.dumps(fn(args)), flush=True)
@@ -417,9 +419,15 @@ def other_workloads(args):
             return bench_demote(a)
         return run
 
+    def prefill_causal(a):  # the prefill workload with the chunk's causal self-attention (GPU line only)
+        a = copy.copy(a)
+        a.no_cpu_baseline = True
+        return bench_prefill(a, causal=True)
+
     for name, fn in (("qwen_decode_4k", bench_c1), ("llama7b_decode_16k", bench_decode_mha),
                      ("llama3_demote_64k", bench_demote), ("llama3_demote_64k_2bit", demote_at(2)),
                      ("llama3_demote_64k_4bit", demote_at(4)), ("llama70b_prefill_128k", bench_prefill),
+                     ("llama70b_prefill_128k_causal", prefill_causal),
                      ("production_decode_4k", bench_production), ("kivi_decode_4k", bench_kivi)):
         print(f"[bench] workload {name}", file=sys.stderr, flush=True)
         try:
@@ -757,7 +765,9 @@ def _workload_dispatches(disp, steps, warmup):
             big = max(g for g, _, _ in ds)  # the demotion launch covers 16 x 8 heads; the headline's own build less
             out[("llama3_demote_64k", "all")] = (key, [d for d in ds if d[0] == big])
         elif key.startswith("prefill_kernel"):
-            out[("llama70b_prefill_128k", "all")] = (key, ds)
+            half = len(ds) // 2  # the plain workload's launches, then as many of the causal one's
+            out[("llama70b_prefill_128k", "all")] = (key, ds[:half])
+            out[("llama70b_prefill_128k_causal", "all")] = (key, ds[half:])
         elif key == "calibration copy":
             out[("calibration", "all")] = (key, ds[-1:])
     return out
@@ -874,9 +884,11 @@ def bench_decode_mha(args):
     return res
 
 
-def bench_prefill(args):
+def bench_prefill(args, causal=False):
     """Chunked prefill, Llama-3-70B attention shape: 512 bf16 queries x 64 heads over
-    131072 cached tokens (4096 hot fp16 + 126976 warm at 2/2 bits), batch 1."""
+    131072 cached tokens (4096 hot fp16 + 126976 warm at 2/2 bits), batch 1; with
+    ``causal`` the chunk's own 512 bf16 keys/values are attended too, position m seeing
+    chunk tokens 0..m."""
     import numpy as np
     import torch
     import akv
@@ -889,21 +901,30 @@ def bench_prefill(args):
     (kw, vw), (kh, vh) = wl.split_hot_warm(k, v, s.n_hot)
     warm = akv.quantize_kv(kw, vw, s.bits_k, s.bits_v, s.block_t, s.group_v)
     del k, v, kw, vw
+    kc = vc = None
+    if causal:
+        gen = torch.Generator(device="cuda").manual_seed(1)
+        kc, vc = (torch.randn(s.B, s.Hkv, s.M, s.D, generator=gen, device="cuda").to(torch.bfloat16) for _ in range(2))
     torch.cuda.synchronize()
-    ms, wall_ms = _event_time(lambda: akv.prefill_attention(q, kh, vh, warm), args.steps, args.warmup)
-    flops = 4.0 * s.Hq * s.M * s.N * s.D * s.B
+    ms, wall_ms = _event_time(lambda: akv.prefill_attention(q, kh, vh, warm, k_chunk=kc, v_chunk=vc),
+                              args.steps, args.warmup)
+    # flops of the attended (query, key) pairs: every cached token, plus chunk tokens 0..m for position m
+    flops = 4.0 * s.Hq * s.D * s.B * (s.M * s.N + (s.M * (s.M + 1) // 2 if causal else 0))
     tflops = flops / (ms * 1e-3) / 1e12
-    res = {"metric": "chunked-prefill attention TFLOP/s at 128K ctx (Llama-3-70B shape), 1xMI355X",
+    res = {"metric": "chunked-prefill attention TFLOP/s at 128K ctx (Llama-3-70B shape), 1xMI355X" +
+                     (", with the chunk's causal self-attention" if causal else ""),
            "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(wall_ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "dtype": "f16", "data": "synthetic (seeded N(0,1) K/V, bf16 queries, quantized on the device)",
-           "config": {"workload": s.name, "B": s.B, "Hq": s.Hq, "Hkv": s.Hkv, "D": s.D, "M": s.M,
-                      "context": s.N, "n_hot": s.n_hot, "n_warm": s.n_warm, "bits_k": s.bits_k, "bits_v": s.bits_v},
+           "config": {"workload": s.name + ("_causal" if causal else ""), "B": s.B, "Hq": s.Hq, "Hkv": s.Hkv,
+                      "D": s.D, "M": s.M, "context": s.N, "n_hot": s.n_hot, "n_warm": s.n_warm, "bits_k": s.bits_k,
+                      "bits_v": s.bits_v, "causal_chunk": causal},
            "ms_per_call": round(ms, 4),
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
-                        "frac": round(tflops / 2500.0, 4), "traffic": recorded_traffic(s.name),
+                        "frac": round(tflops / 2500.0, 4),
+                        "traffic": recorded_traffic(s.name) if not causal else None,
                         "kernel": "prefill_kernel (one launch at this shape)", "flops_per_launch": flops}}
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not causal:  # the CPU sample is of the cache part only
         # torch CPU restatement: dequant + fp32 attention of kv-head 0's 8 query heads at 16 positions
         host = {n: getattr(warm, n)[:, :1].cpu() for n in ("k_codes", "k_scale", "k_zero", "v_codes", "v_scale",
                                                            "v_zero")}

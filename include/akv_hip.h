@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define AKV_ABI_VERSION 4
+#define AKV_ABI_VERSION 5
 
 /* status codes */
 #define AKV_OK 0
@@ -291,6 +291,9 @@ typedef struct akv_prefill_args {
     void *out;             /* [B][Hq][M][D], q dtype */
     void *workspace;       /* akv_prefill_workspace_bytes() bytes (0 with a single split) */
     int64_t workspace_bytes;
+    const void *k_chunk, *v_chunk; /* optional [B][Hkv][M][D] in q's dtype: the chunk's own keys and
+                              values, attended after the cache with a causal mask (query position m
+                              sees chunk tokens 0..m); both NULL = the cache only */
 } akv_prefill_args;
 
 /* Bytes of device workspace akv_prefill_attn needs for `args` (split partials). */
@@ -298,8 +301,10 @@ int64_t akv_prefill_workspace_bytes(const akv_prefill_args *args);
 
 /* Chunked prefill: M query positions per head (a prompt chunk after every
  * cached token, so no mask over the cache) attend to the hot fp16 + warm
- * block-affine cache; no attention weights.  QK^T and PV run on MFMA over
- * dequantized LDS tiles shared by the GQA group's heads.
+ * block-affine cache and, when k_chunk / v_chunk are given, causally to the
+ * chunk's own tokens; no attention weights.  QK^T and PV run on MFMA over
+ * dequantized LDS tiles shared by the GQA group's heads.  The causal part has
+ * no counterpart in the reference (its attention over a chunk is the model's).
  * Replaces, for M > 1 without weights: triton_ops.fused_quantized_attention
  * (akv/triton_ops.py:330-377) and triton_ops.fused_mixed_precision_attention
  * (akv/triton_ops.py:466-515), which dequantize the whole warm tier first. */

@@ -209,3 +209,24 @@ def test_prefill_planning_and_checks():
     assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_UNSUPPORTED
     a = _prefill_args(nat, M=16, num_splits=3)
     assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_WORKSPACE
+
+
+def test_prefill_chunk_kv_checks():
+    """The chunk's own K / V (causal part) come as a pair, 16-byte aligned, and
+    alone are enough tokens to attend to; their tiles join the token splits."""
+    from akv import _native as nat
+    lib = nat.load()
+    a = _prefill_args(nat, k_chunk=0x30000)
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) == -1
+    assert b"k_chunk and v_chunk go together" in lib.akv_last_error()
+    a = _prefill_args(nat, k_chunk=0x30000, v_chunk=0x30008)
+    assert lib.akv_prefill_attn(ctypes.byref(a), None) == nat.AKV_E_ALIGN
+    a = _prefill_args(nat, n_hot=0)
+    a.warm.kind = nat.WARM_NONE
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) == -1
+    assert b"no tokens" in lib.akv_last_error()
+    a = _prefill_args(nat, n_hot=0, k_chunk=0x30000, v_chunk=0x40000)
+    a.warm.kind = nat.WARM_NONE
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) >= 0
+    a = _prefill_args(nat, k_chunk=0x30000, v_chunk=0x40000)
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(a)) >= 0

@@ -112,3 +112,101 @@ def test_prefill_llama70b_128k_slice():
     bound = 2e-3 + np.abs(ref) * 2.0 ** -9
     assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
     assert err.mean() <= 1e-3
+
+
+def _chunk_kv(B, Hkv, M, seed, dtype=torch.float16):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(B, Hkv, M, 128, generator=g).to(dtype), torch.randn(B, Hkv, M, 128, generator=g).to(dtype))
+
+
+@pytest.mark.parametrize("M,ns", [(24, 0), (40, 0), (33, 3), (70, 5)])
+def test_prefill_causal_chunk(M, ns):
+    """The chunk's own K/V after the cache, causal: position m sees chunk tokens 0..m
+    (ragged last chunk tiles, chunk tiles spread over token splits)."""
+    announce(f"prefill causal chunk M={M} splits={ns}")
+    q, kh, vh, w, kd, vd = _case(2, 8, 2, 40, 200, 3, 3, M=M, seed=7)
+    kq, vq = _chunk_kv(2, 2, M, seed=M)
+    out = _prefill(q.numpy(), kh, vh, w, num_splits=ns, k_chunk=to_dev(kq), v_chunk=to_dev(vq))
+    kcache = np.concatenate([kh, kd.astype(np.float16)], axis=2)
+    vcache = np.concatenate([vh, vd.astype(np.float16)], axis=2)
+    ref = oatt.prefill_causal_fp32(q.numpy(), kcache, vcache, kq.numpy(), vq.numpy())
+    assert_close_attn(out, ref)
+
+
+@pytest.mark.parametrize("M,ns", [(100, 13), (100, 11), (80, 6)])
+def test_prefill_causal_masked_splits(M, ns):
+    """Token splits that begin past the chunk's first tile: early positions see no token
+    of such a split (its partial must weigh nothing in the merge).  13 tiles (2 hot,
+    7 warm, 4 chunk at M=100) in 13 / 7 splits (asked for 11), and 12 tiles (M=80) in 6."""
+    announce(f"prefill causal chunk, fully masked splits M={M} splits={ns}")
+    q, kh, vh, w, kd, vd = _case(1, 8, 2, 40, 200, 3, 3, M=M, seed=12)
+    kq, vq = _chunk_kv(1, 2, M, seed=13)
+    out = _prefill(q.numpy(), kh, vh, w, num_splits=ns, k_chunk=to_dev(kq), v_chunk=to_dev(vq))
+    kcache = np.concatenate([kh, kd.astype(np.float16)], axis=2)
+    vcache = np.concatenate([vh, vd.astype(np.float16)], axis=2)
+    ref = oatt.prefill_causal_fp32(q.numpy(), kcache, vcache, kq.numpy(), vq.numpy())
+    assert np.isfinite(out.float().cpu().numpy()).all()
+    assert_close_attn(out, ref)
+
+
+def test_prefill_causal_chunk_only_splits():
+    """The chunk alone (no cache) over several token splits: rows before a split's first
+    token get nothing from it."""
+    announce("prefill causal chunk alone, 4 splits")
+    q, _, _, _, _, _ = _case(1, 8, 1, 32, 96, 3, 3, M=128, seed=14)
+    kq, vq = _chunk_kv(1, 1, 128, seed=15)
+    out = _prefill(q.numpy(), None, None, None, num_splits=4, k_chunk=to_dev(kq), v_chunk=to_dev(vq))
+    ref = oatt.prefill_causal_fp32(q.numpy(), None, None, kq.numpy(), vq.numpy())
+    assert np.isfinite(out.float().cpu().numpy()).all()
+    assert_close_attn(out, ref)
+
+
+def test_prefill_causal_chunk_bf16_and_chunk_only():
+    announce("prefill causal chunk bf16, and the chunk alone")
+    q, kh, vh, w, kd, vd = _case(1, 4, 1, 32, 96, 4, 2, M=36, seed=8)
+    qb = q.to(torch.bfloat16)
+    kq, vq = _chunk_kv(1, 1, 36, seed=9, dtype=torch.bfloat16)
+    out = _prefill(qb, kh, vh, w, k_chunk=to_dev(kq), v_chunk=to_dev(vq))
+    assert out.dtype == torch.bfloat16
+    kcache = np.concatenate([kh, kd.astype(np.float16)], axis=2)
+    vcache = np.concatenate([vh, vd.astype(np.float16)], axis=2)
+    ref = oatt.prefill_causal_fp32(qb.float().numpy(), kcache, vcache, kq.float().numpy(), vq.float().numpy())
+    got = out.float().cpu().numpy()
+    err = np.abs(got - ref)
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -9
+    assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
+    assert err.mean() <= 1e-3
+    # no cache at all: the chunk's causal self-attention alone
+    kq16, vq16 = _chunk_kv(1, 1, 36, seed=10)
+    out = _prefill(q.numpy(), None, None, None, k_chunk=to_dev(kq16), v_chunk=to_dev(vq16))
+    ref = oatt.prefill_causal_fp32(q.numpy(), None, None, kq16.numpy(), vq16.numpy())
+    assert_close_attn(out, ref)
+
+
+def test_prefill_llama70b_128k_causal_slice():
+    """The 128k workload with the chunk's causal self-attention at full size; the oracle
+    checks kv-head 0's 8 query heads at the chunk's first and last 32 positions."""
+    import akv
+    from akv import workloads as wl
+    announce("prefill Llama-70B 128k full size, causal chunk")
+    sh = wl.LLAMA70B_PREFILL_128K
+    k, v = wl.make_kv(sh, device="cuda")
+    q = wl.make_q(sh, device="cuda", dtype=torch.bfloat16)
+    (kw, vw), (kh, vh) = wl.split_hot_warm(k, v, sh.n_hot)
+    wt = akv.quantize_kv(kw, vw, sh.bits_k, sh.bits_v, sh.block_t, sh.group_v)
+    kq, vq = (t.to("cuda") for t in _chunk_kv(sh.B, sh.Hkv, sh.M, seed=11, dtype=torch.bfloat16))
+    out = akv.prefill_attention(q, kh, vh, wt, k_chunk=kq, v_chunk=vq)
+    torch.cuda.synchronize()
+    kd, vd = akv.dequantize(wt)
+    g = sh.Hq // sh.Hkv
+    sel = np.concatenate([np.arange(32), np.arange(sh.M - 32, sh.M)])
+    qs = q[:, :g, sel].float().cpu().numpy()
+    kcache = np.concatenate([kh[:, :1].cpu().numpy(), kd[:, :1].cpu().numpy()], axis=2)
+    vcache = np.concatenate([vh[:, :1].cpu().numpy(), vd[:, :1].cpu().numpy()], axis=2)
+    ref = oatt.prefill_causal_fp32(qs, kcache, vcache, kq[:, :1].float().cpu().numpy(),
+                                   vq[:, :1].float().cpu().numpy(), positions=sel)
+    got = out[:, :g, sel].float().cpu().numpy()
+    err = np.abs(got - ref)
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -9
+    assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
+    assert err.mean() <= 1e-3
