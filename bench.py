@@ -19,8 +19,9 @@ The line's "workloads" field summarises the other configurations, each
 measured after the headline on its own inputs (metric, value, roofline, CPU
 baseline): qwen_decode_4k (one Qwen layer at 4k context, 4/4-bit, with the
 reference CPU path beside it), llama7b_decode_16k (MHA, K4/V2 with outlier
-channels), llama3_demote_64k (select + gather + quantize + pack, 3-bit),
-llama70b_prefill_128k (MFMA chunked prefill) and production_decode_4k
+channels), llama3_demote_64k (select + gather + quantize + pack, 3-bit; and
+at 2 and 4 bits), llama70b_prefill_128k (MFMA chunked prefill; and with the
+chunk's causal self-attention) and production_decode_4k
 (ProductionCache.fused_attention over the 4-bit arenas at the cache's default
 sizes, with the reference's torch design timed beside it) and kivi_decode_4k
 (the KIVI baseline's attention at the same sizes, 2 bits).  --workload NAME
@@ -764,10 +765,9 @@ def _workload_dispatches(disp, steps, warmup):
         elif key.startswith("quant_fast_kernel<3, 3,"):
             big = max(g for g, _, _ in ds)  # the demotion launch covers 16 x 8 heads; the headline's own build less
             out[("llama3_demote_64k", "all")] = (key, [d for d in ds if d[0] == big])
-        elif key.startswith("prefill_kernel"):
-            half = len(ds) // 2  # the plain workload's launches, then as many of the causal one's
-            out[("llama70b_prefill_128k", "all")] = (key, ds[:half])
-            out[("llama70b_prefill_128k_causal", "all")] = (key, ds[half:])
+        elif key.startswith("prefill_kernel"):  # the causal variant is the instantiation ending in "true"
+            causal = key.endswith("true>")
+            out[("llama70b_prefill_128k_causal" if causal else "llama70b_prefill_128k", "all")] = (key, ds)
         elif key == "calibration copy":
             out[("calibration", "all")] = (key, ds[-1:])
     return out
@@ -922,7 +922,7 @@ def bench_prefill(args, causal=False):
            "ms_per_call": round(ms, 4),
            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": 2500.0, "unit": "TFLOP/s",
                         "frac": round(tflops / 2500.0, 4),
-                        "traffic": recorded_traffic(s.name) if not causal else None,
+                        "traffic": recorded_traffic(s.name + ("_causal" if causal else "")),
                         "kernel": "prefill_kernel (one launch at this shape)", "flops_per_launch": flops}}
     if not args.no_cpu_baseline and not causal:  # the CPU sample is of the cache part only
         # torch CPU restatement: dequant + fp32 attention of kv-head 0's 8 query heads at 16 positions
