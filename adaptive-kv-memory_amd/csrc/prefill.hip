@@ -49,6 +49,7 @@ constexpr int kVzTile = 2 * 64 * 8;            // 1024
 constexpr int kBuf = kKTile + kVTile + kVzTile;
 constexpr int kPKmeta = 3 * 4 * 16 * 4;        // [s | n | z][group][pair] u32, per K wave
 constexpr int kPLds = 2 * kBuf + 4 * kPKmeta;
+constexpr uint32_t kOnes2 = 0x3C003C00u;       // fp16 pair (1, 1)
 
 // bf16 pair (one dword) -> fp16 pair (exact for values in fp16's normal range)
 __device__ __forceinline__ uint32_t bf16x2_to_h2(uint32_t w) {
@@ -250,6 +251,8 @@ void prefill_kernel(const PrefillParams p) {
                     *(uint32_t *)(vt + (((kk * 2 + vh) * 2 + vp) * 64 + lane) * 4) =
                         perm(hraw[1][kk / 2], hraw[0][kk / 2], sel);
                 }
+                // zeros operand of a hot tile: no zero-points; chunk row 15 takes ones (row sums)
+                *(uint32_t *)(vzt + ((vh * 2 + vp) * 64 + lane) * 4) = col == 15 ? kOnes2 : 0u;
             }
             return;
         }
@@ -339,7 +342,8 @@ void prefill_kernel(const PrefillParams p) {
             }
 #pragma unroll
             for (int kk = 0; kk < 8; ++kk) *(uint32_t *)(vt + (((kk * 2 + vh) * 2 + vp) * 64 + lane) * 4) = vpair[kk];
-            *(uint32_t *)(vzt + ((vh * 2 + vp) * 64 + lane) * 4) = as_u32(vz);
+            // chunk row 15 takes ones: that row of the zeros MFMA gives the row sums of P
+            *(uint32_t *)(vzt + ((vh * 2 + vp) * 64 + lane) * 4) = col == 15 ? kOnes2 : as_u32(vz);
         }
     };
 
@@ -393,16 +397,11 @@ void prefill_kernel(const PrefillParams p) {
             sm[1].acc[kk] = mfma_k32(a, pop[1], sm[1].acc[kk]);
         }
         {
-            // zeros MFMA: chunk rows 0-14 take the tile's zero-points (none for hot
-            // tiles); chunk row 15 takes ones, so its output is the row sum of P (l).
-            // Chunks 12-15 share one V group, so chunk 15's zero term is chunk 12's.
-            u4 zw = {0u, 0u, 0u, 0u};
-            if (!hot) {
-                const uint32_t *za = (const uint32_t *)(vzt + lane * 4);
-                zw = (u4){za[0], za[64], za[128], za[192]};
-            }
-            if (col == 15) zw = (u4){0x3C003C00u, 0x3C003C00u, 0x3C003C00u, 0x3C003C00u};
-            const h8 az = __builtin_bit_cast(h8, zw);
+            // zeros MFMA: chunk rows 0-14 take the tile's zero-points (zero for hot tiles);
+            // chunk row 15 takes ones, so its output is the row sum of P (l); the staging
+            // wrote both.  Chunks 12-15 share one V group, so chunk 15's zero term is chunk 12's.
+            const uint32_t *za = (const uint32_t *)(vzt + lane * 4);
+            const h8 az = __builtin_bit_cast(h8, (u4){za[0], za[64], za[128], za[192]});
             sm[0].accz = mfma_k32(az, pop[0], sm[0].accz);
             sm[1].accz = mfma_k32(az, pop[1], sm[1].accz);
         }
