@@ -158,6 +158,9 @@ int check_decode(const akv_decode_args *a) {
     if (a->B < 1 || a->Hq < 1 || a->Hkv < 1 || a->M < 1)
         return fail(AKV_E_SHAPE, "B, Hq, Hkv, M must be >= 1");
     if (a->Hq % a->Hkv) return fail(AKV_E_SHAPE, "Hq (%d) must be a multiple of Hkv (%d)", a->Hq, a->Hkv);
+    // the online softmax takes the largest raw score as the largest scaled one
+    if (!(a->sm_scale > 0.0f) || !(a->sm_scale < INFINITY))
+        return fail(AKV_E_INVALID, "sm_scale must be positive and finite (got %g)", (double)a->sm_scale);
     if (a->n_hot < 0) return fail(AKV_E_SHAPE, "n_hot < 0");
     const akv_warm_desc &w = a->warm;
     const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;
@@ -228,6 +231,9 @@ int check_prefill(const akv_prefill_args *a) {
     if (a->D != 128) return fail(AKV_E_SHAPE, "prefill supports head_dim 128 (got %d)", a->D);
     if (a->B < 1 || a->Hq < 1 || a->Hkv < 1 || a->M < 1) return fail(AKV_E_SHAPE, "B, Hq, Hkv, M must be >= 1");
     if (a->Hq % a->Hkv) return fail(AKV_E_SHAPE, "Hq (%d) must be a multiple of Hkv (%d)", a->Hq, a->Hkv);
+    // the online softmax takes the largest raw score as the largest scaled one
+    if (!(a->sm_scale > 0.0f) || !(a->sm_scale < INFINITY))
+        return fail(AKV_E_INVALID, "sm_scale must be positive and finite (got %g)", (double)a->sm_scale);
     if (a->n_hot < 0) return fail(AKV_E_SHAPE, "n_hot < 0");
     const akv_warm_desc &w = a->warm;
     const int64_t nw = w.kind == AKV_WARM_NONE ? 0 : w.n_warm;

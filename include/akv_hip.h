@@ -103,7 +103,7 @@ typedef struct akv_decode_args {
     const void *k_hot, *v_hot; /* [B][Hkv][n_hot][D], q dtype (may be NULL when n_hot == 0) */
     int64_t n_hot;
     int32_t hot_first;     /* token order: 1 = [hot, warm] (reference ops), 0 = [warm, hot] */
-    float sm_scale;        /* softmax scale (1/sqrt(D) in the reference) */
+    float sm_scale;        /* softmax scale (1/sqrt(D) in the reference); > 0 */
     akv_warm_desc warm;
     void *out;             /* [B][Hq][M][D], q dtype */
     float *attn_weights;   /* optional [B][Hq][M][N] fp32, N = n_hot + n_warm, 16-byte aligned */
@@ -284,7 +284,7 @@ typedef struct akv_prefill_args {
     const void *q;         /* [B][Hq][M][D] */
     const void *k_hot, *v_hot; /* [B][Hkv][n_hot][D] f16 (may be NULL when n_hot == 0) */
     int64_t n_hot;
-    float sm_scale;        /* softmax scale (1/sqrt(D) in the reference) */
+    float sm_scale;        /* softmax scale (1/sqrt(D) in the reference); > 0 */
     int32_t num_splits;    /* token splits, 0 = choose */
     akv_warm_desc warm;    /* AKV_WARM_NONE, or AKV_WARM_AFFINE with block_t % 32 == 0,
                               group_v in {32, 64, 128} and n_out == 0 */

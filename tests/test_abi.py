@@ -75,6 +75,7 @@ def test_decode_shape_checks():
     a.q_dtype = nat.DT_F16
     a.B, a.Hq, a.Hkv, a.M, a.D = 1, 12, 5, 1, 128
     a.n_hot = 4
+    a.sm_scale = 128 ** -0.5
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1
     assert b"multiple of Hkv" in lib.akv_last_error()
     a.Hkv, a.D = 2, 96
@@ -88,6 +89,14 @@ def test_decode_shape_checks():
     assert b"attn_weights must be 16-byte aligned" in lib.akv_last_error()
     a.attn_weights = 0x10010
     assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) > 0
+    # the online softmax needs a positive, finite scale
+    for bad in (0.0, -0.1, float("inf"), float("nan")):
+        a.sm_scale = bad
+        assert lib.akv_decode_workspace_bytes(ctypes.byref(a)) == -1
+        assert b"sm_scale must be positive" in lib.akv_last_error()
+    b = _prefill_args(nat, sm_scale=-1.0)
+    assert lib.akv_prefill_workspace_bytes(ctypes.byref(b)) == -1
+    assert b"sm_scale must be positive" in lib.akv_last_error()
 
 
 def test_legacy_warm_heads_and_strides():
@@ -100,6 +109,7 @@ def test_legacy_warm_heads_and_strides():
     a.abi_version = nat.ABI_VERSION
     a.q_dtype = nat.DT_F16
     a.B, a.Hq, a.Hkv, a.M, a.D = 3, 8, 4, 1, 128
+    a.sm_scale = 128 ** -0.5
     a.q = a.out = 0x10000  # host-side checks only: never dereferenced
     w = a.warm
     w.kind = nat.WARM_LEGACY
