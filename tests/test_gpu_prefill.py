@@ -2,7 +2,8 @@
 
 Tolerance (from the task statement): 2e-3 max-abs, 1e-3 mean-abs against the
 fp32 attention over the oracle's fp16 dequantized K/V.  bf16 outputs add the
-rounding of the output itself: half an ulp of bf16 (2^-9 relative) per value."""
+rounding of the output itself: half an ulp of bf16, at most 2^-8 of the value (8
+significant bits; the bound is reached at the bottom of a binade)."""
 import numpy as np
 import pytest
 import torch
@@ -60,7 +61,7 @@ def test_prefill_bf16_queries_and_group_sizes():
     ref, _ = oatt.mixed_attention_fp32(qb.float().numpy(), kh, vh, kd, vd, return_weights=False)
     got = out.float().cpu().numpy()
     err = np.abs(got - ref)
-    bound = 2e-3 + np.abs(ref) * 2.0 ** -9
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -8
     assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
     assert err.mean() <= 1e-3
 
@@ -109,7 +110,7 @@ def test_prefill_llama70b_128k_slice():
                                        kd[:, :1].cpu().numpy(), vd[:, :1].cpu().numpy(), return_weights=False)
     got = out[:, :g, :64].float().cpu().numpy()
     err = np.abs(got - ref)
-    bound = 2e-3 + np.abs(ref) * 2.0 ** -9
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -8
     assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
     assert err.mean() <= 1e-3
 
@@ -149,6 +150,31 @@ def test_prefill_causal_masked_splits(M, ns):
     assert_close_attn(out, ref)
 
 
+def test_prefill_causal_single_position_and_row_tiles():
+    """M = 1: the one new token sees the whole cache and itself (plain attention over
+    cache + that token).  M = 300 with 8 query heads per kv head: 2,400 rows per
+    (batch, kv-head), ten 256-row tiles, the last one partial; B = 2, bf16."""
+    announce("prefill causal chunk M=1, and M=300 over ten row tiles (bf16, B=2)")
+    q, kh, vh, w, kd, vd = _case(1, 4, 2, 40, 200, 3, 3, M=1, seed=16)
+    kq, vq = _chunk_kv(1, 2, 1, seed=17)
+    out = _prefill(q.numpy(), kh, vh, w, k_chunk=to_dev(kq), v_chunk=to_dev(vq))
+    kall = np.concatenate([kh, kd.astype(np.float16), kq.numpy()], axis=2)
+    vall = np.concatenate([vh, vd.astype(np.float16), vq.numpy()], axis=2)
+    ref, _ = oatt.attention_fp32(q.numpy(), kall, vall, return_weights=False)
+    assert_close_attn(out, ref)
+    q, kh, vh, w, kd, vd = _case(2, 16, 2, 64, 320, 2, 2, M=300, seed=18)
+    qb = q.to(torch.bfloat16)
+    kq, vq = _chunk_kv(2, 2, 300, seed=19, dtype=torch.bfloat16)
+    out = _prefill(qb, kh, vh, w, k_chunk=to_dev(kq), v_chunk=to_dev(vq))
+    kcache = np.concatenate([kh, kd.astype(np.float16)], axis=2)
+    vcache = np.concatenate([vh, vd.astype(np.float16)], axis=2)
+    ref = oatt.prefill_causal_fp32(qb.float().numpy(), kcache, vcache, kq.float().numpy(), vq.float().numpy())
+    err = np.abs(out.float().cpu().numpy() - ref)
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -8
+    assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
+    assert err.mean() <= 1e-3
+
+
 def test_prefill_causal_chunk_only_splits():
     """The chunk alone (no cache) over several token splits: rows before a split's first
     token get nothing from it."""
@@ -173,7 +199,7 @@ def test_prefill_causal_chunk_bf16_and_chunk_only():
     ref = oatt.prefill_causal_fp32(qb.float().numpy(), kcache, vcache, kq.float().numpy(), vq.float().numpy())
     got = out.float().cpu().numpy()
     err = np.abs(got - ref)
-    bound = 2e-3 + np.abs(ref) * 2.0 ** -9
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -8
     assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
     assert err.mean() <= 1e-3
     # no cache at all: the chunk's causal self-attention alone
@@ -207,6 +233,6 @@ def test_prefill_llama70b_128k_causal_slice():
                                    vq[:, :1].float().cpu().numpy(), positions=sel)
     got = out[:, :g, sel].float().cpu().numpy()
     err = np.abs(got - ref)
-    bound = 2e-3 + np.abs(ref) * 2.0 ** -9
+    bound = 2e-3 + np.abs(ref) * 2.0 ** -8
     assert (err <= bound).all(), f"max excess {np.max(err - bound):.3e}"
     assert err.mean() <= 1e-3
