@@ -57,3 +57,24 @@ def test_passthrough_widths():
     assert bp.packed_bytes(codes, 4) == 4 * 8
     assert bp.packed_bytes(codes, 3) == 4 * 6
     assert bp.packed_bytes(codes, 8) == 64
+
+
+@pytest.mark.parametrize("dim", [8, 13, 128])
+def test_per_width_functions(dim):
+    """The reference's per-width entry points (pack_uint4 / unpack_uint4, pack_uint3 /
+    unpack_uint3, pack_uint2 / unpack_uint2) equal the oracle's byte for byte; like the
+    reference's, 2-bit unpacking takes only lengths that are multiples of 4."""
+    import akv.bitpack as bp
+    announce(f"bitpack per-width functions dim={dim}")
+    rng = np.random.default_rng(7 * dim)
+    for bits, pk, upk, opk in ((4, bp.pack_uint4, bp.unpack_uint4, obp.pack_uint4),
+                               (3, bp.pack_uint3, bp.unpack_uint3, obp.pack_uint3),
+                               (2, bp.pack_uint2, bp.unpack_uint2, obp.pack_uint2)):
+        codes = rng.integers(0, 1 << bits, size=(2, 3, dim), dtype=np.uint8)
+        packed = pk(to_dev(codes))
+        np.testing.assert_array_equal(packed.cpu().numpy(), opk(codes))
+        if bits == 2 and dim % 4:
+            with pytest.raises(ValueError):
+                upk(packed, dim)
+            continue
+        np.testing.assert_array_equal(upk(packed, dim).cpu().numpy(), codes)
