@@ -187,3 +187,20 @@ def test_kvquantizer(bits, gs, sym):
     bits_equal(qt.scales, ref["scales"])
     bits_equal(qt.zeros, ref["zeros"])
     bits_equal(qz.dequantize(qt), oleg.kvq_dequantize(ref))
+
+
+def test_kvquantizer_error_and_compression():
+    """KVQuantizer.estimate_error is the MSE of the device round trip (more bits, less
+    error), and QuantizedTensor.compression_ratio is fp16 bytes over stored bytes."""
+    import akv
+    announce("KVQuantizer estimate_error / compression_ratio")
+    torch.manual_seed(42)
+    t = torch.randn(1, 4, 32, 64, dtype=torch.float16).cuda()
+    q = akv.KVQuantizer(akv.QuantConfig(group_size=32))
+    errs = {b: q.estimate_error(t, bits=b) for b in (2, 4, 8)}
+    assert errs[8] < errs[4] < errs[2]
+    rec = q.dequantize(q.quantize(t, bits=4))
+    assert errs[4] == (t.float() - rec.float()).pow(2).mean().item()
+    qt = akv.KVQuantizer(akv.QuantConfig(bits=4, group_size=32)).quantize(t)
+    assert qt.compression_ratio == (1 * 4 * 32 * 64 * 2) / qt.nbytes
+    assert qt.compression_ratio > 2.0

@@ -84,3 +84,20 @@ def test_decode_workspace_tracks_the_last_counter_region():
     buf[512:] = 3
     assert ws.get(4096, 512, "cpu") is buf and int(buf[:512].sum()) == 0
     assert ws.get(8192, 256, "cpu").numel() >= 8192  # grows when a call needs more bytes
+
+
+def test_estimate_memory_savings_closed_form():
+    """KVQuantizer.estimate_memory_savings (akv/quantizer.py:256-272) at 32 layers x 32
+    heads x 4096 tokens x 128: fp16 K and V 2,147,483,648 B; 4-bit data 536,870,912 B;
+    one group of 128 -> fp16 scale + zero per (layer, K/V, head, token) 33,554,432 B."""
+    import akv
+    q = akv.KVQuantizer(akv.QuantConfig(bits=4, group_size=128))
+    s = q.estimate_memory_savings(num_layers=32, num_heads=32, seq_len=4096, head_dim=128, bits=4)
+    assert s["original_mb"] == 2147.483648
+    assert abs(s["quantized_mb"] - 570.425344) < 1e-9
+    assert abs(s["savings_mb"] - (2147.483648 - 570.425344)) < 1e-9
+    assert abs(s["compression_ratio"] - 2147483648 / 570425344) < 1e-12
+    # 2 bits with groups of 32: 4 groups per row, data a quarter byte per value
+    s = akv.KVQuantizer(akv.QuantConfig(bits=2, group_size=32)).estimate_memory_savings(1, 1, 10, 128)
+    assert s["original_mb"] == 1 * 2 * 1 * 10 * 128 * 2 / 1e6
+    assert abs(s["quantized_mb"] - (2 * 10 * 128 * 2 / 8 + 2 * 10 * 4 * 4) / 1e6) < 1e-12
