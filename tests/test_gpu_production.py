@@ -206,3 +206,42 @@ def test_batched_queries_one_launch_and_hot_accounting():
     with pytest.raises(RuntimeError, match="exhausted"):
         lay.append_hot(torch.zeros(H, 8 * 16 - lay.hot_len + 1, D, dtype=torch.float16, device="cuda"),
                        torch.zeros(H, 8 * 16 - lay.hot_len + 1, D, dtype=torch.float16, device="cuda"))
+
+
+def test_layer_cache_accessors_and_demotion():
+    """ProductionLayerCache's own methods (akv/production_cache.py:182-320): append_hot /
+    get_hot_kv return the appended rows; demote_to_warm quantizes the given rows into the
+    arenas (bit-exact with the oracle's arena quantizer), drops the demoted positions from
+    the hot tier keeping the others in order, and get_warm_fp16 / get_warm_packed expose
+    the arenas (dequantized / as stored)."""
+    from akv.production_cache import ProductionLayerCache
+    from oracle import legacy as olg
+    announce("ProductionLayerCache append / demote / warm views")
+    cfg = _config(4, 64)
+    layer = ProductionLayerCache(cfg, 0)
+    assert layer.hot_capacity == cfg.page_size * cfg.max_hot_pages
+    assert layer.get_warm_fp16() == (None, None)
+    assert layer.get_warm_packed() == (None,) * 6
+    rng = np.random.default_rng(21)
+    k, v = _rows(rng, 4, 30, 128), _rows(rng, 4, 30, 128)
+    layer.append_hot(to_dev(k, torch.float16), to_dev(v, torch.float16))
+    hk, hv = layer.get_hot_kv()
+    bits_equal(hk, k.astype(np.float16))
+    bits_equal(hv, v.astype(np.float16))
+    idx = np.array([0, 3, 4, 17, 29])
+    layer.demote_to_warm(to_dev(idx, torch.long), to_dev(k[:, idx], torch.float16), to_dev(v[:, idx], torch.float16))
+    keep = np.setdiff1d(np.arange(30), idx)
+    hk, hv = layer.get_hot_kv()
+    bits_equal(hk, k[:, keep].astype(np.float16))
+    bits_equal(hv, v[:, keep].astype(np.float16))
+    pk, sk, zk = olg.arena_quantize(k[:, idx], 4, 64)
+    pv, sv, zv = olg.arena_quantize(v[:, idx], 4, 64)
+    got = layer.get_warm_packed()
+    for g, r in zip(got, (pk, sk, zk, pv, sv, zv)):
+        bits_equal(g, r)
+    wk, wv = layer.get_warm_fp16()
+    bits_equal(wk, olg.arena_dequantize(pk, sk, zk, 4, 64, 128))
+    bits_equal(wv, olg.arena_dequantize(pv, sv, zv, 4, 64, 128))
+    with pytest.raises(RuntimeError, match="Page pool exhausted"):
+        big = to_dev(_rows(rng, 4, layer.hot_capacity, 128), torch.float16)
+        layer.append_hot(big, big)

@@ -101,3 +101,17 @@ def test_estimate_memory_savings_closed_form():
     s = akv.KVQuantizer(akv.QuantConfig(bits=2, group_size=32)).estimate_memory_savings(1, 1, 10, 128)
     assert s["original_mb"] == 1 * 2 * 1 * 10 * 128 * 2 / 1e6
     assert abs(s["quantized_mb"] - (2 * 10 * 128 * 2 / 8 + 2 * 10 * 4 * 4) / 1e6) < 1e-12
+
+
+def test_cache_length_queries_and_arena_config():
+    """AKVCache.get_usable_length is the layer's sequence length and get_max_length is
+    None (akv/drop_in.py:1104-1110); PackedKVConfig's derived sizes
+    (akv/packed_layout.py:41-53): values per byte, packed head_dim, groups per row."""
+    import akv
+    from akv.packed_layout import PackedKVConfig
+    cache = akv.AKVCache()
+    assert cache.get_usable_length(4096) == 0 and cache.get_usable_length(16, layer_idx=3) == 0
+    assert cache.get_max_length() is None
+    for bits, pf in ((2, 4), (4, 2), (8, 1)):
+        c = PackedKVConfig(head_dim=128, bits=bits, group_size=48, device="cpu")
+        assert (c.pack_factor, c.packed_dim, c.num_groups) == (pf, 128 // pf, 3)
