@@ -141,6 +141,45 @@ class ImportanceScorer:
     def get_scores(self, layer_idx: int) -> Optional[torch.Tensor]:
         return self._scores.get(layer_idx)
 
+    def get_aggregated_scores(self) -> Optional[torch.Tensor]:
+        """akv/importance.py:174-188: the layers' scores, each zero-padded to the longest,
+        averaged over layers (float32); None before any update."""
+        if not self._scores:
+            return None
+        longest = max(int(s.shape[0]) for s in self._scores.values())
+        dev = next(iter(self._scores.values())).device
+        total = torch.zeros(longest, dtype=torch.float32, device=dev)
+        for s in self._scores.values():
+            total[: s.shape[0]] += s.to(device=dev, dtype=torch.float32)
+        return total / len(self._scores)
+
+    def get_tier_assignments(self, layer_idx: int, seq_len: int, hot_budget: int,
+                             warm_budget: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """akv/importance.py:190-243: positions 0..seq_len-1 split into (hot, warm, cold),
+        each ascending: the ``hot_budget`` most important, the next ``warm_budget``, the
+        rest, with the first ``initial_tokens_protected`` and last
+        ``recent_tokens_protected`` ranked above every scored position.  Without scores
+        the split is by position.  Equal scores rank the lower index as less important,
+        as ``get_eviction_candidates`` does (the reference's argsort leaves their order
+        open)."""
+        scores = self._scores.get(layer_idx)
+        cfg = self.config
+        if scores is None or seq_len == 0:
+            pos = torch.arange(seq_len)
+            h, w = min(hot_budget, seq_len), min(hot_budget + warm_budget, seq_len)
+            return pos[:h], pos[h:w], pos[w:]
+        s = scores[:seq_len].to(torch.float32).clone()
+        n_start = min(cfg.initial_tokens_protected, s.shape[0])
+        n_end = min(cfg.recent_tokens_protected, s.shape[0])
+        s[:n_start] = float("inf")
+        if n_end > 0:
+            s[-n_end:] = float("inf")
+        # least important first (stable: equal scores keep index order), read backwards
+        rank = torch.sort(s, stable=True).indices.flip(0)
+        total = rank.shape[0]
+        h, w = min(hot_budget, total), min(hot_budget + warm_budget, total)
+        return rank[:h].sort().values, rank[h:w].sort().values, rank[w:].sort().values
+
     def get_eviction_candidates(self, layer_idx: int, seq_len: int, num_to_evict: int) -> torch.Tensor:
         """akv/importance.py:245-300: ascending indices of the ``num_to_evict`` least
         important of the first ``seq_len`` positions, the first

@@ -55,3 +55,23 @@ def test_default_scorer_is_hybrid_and_updates():
     s = sc.get_scores(0)
     assert s.shape == (16,) and torch.isfinite(s).all()
     assert float(s.max()) <= 0.7 + 0.3 + 1e-6  # normalised EMA (<= 0.7) plus recency (<= 0.3)
+
+
+def test_aggregated_scores_and_tiers_on_device():
+    """After device updates of two layers: the aggregate is the layers' mean on the device,
+    and the tier split of a layer is taken on its scores' device."""
+    from akv.importance import ImportanceConfig, ImportanceScorer, ScoringStrategy
+    announce("ImportanceScorer aggregate / tiers on the device")
+    sc = ImportanceScorer(ImportanceConfig(strategy=ScoringStrategy.ATTENTION_ACCUMULATION,
+                                           initial_tokens_protected=2, recent_tokens_protected=2))
+    rng = np.random.default_rng(3)
+    a = rng.random((1, 2, 1, 16)).astype(np.float32)
+    a /= a.sum(-1, keepdims=True)
+    sc.update(to_dev(a), layer_idx=0)
+    sc.update(to_dev(a * 0.5), layer_idx=1)
+    agg = sc.get_aggregated_scores()
+    assert agg.is_cuda and agg.shape == (16,)
+    torch.testing.assert_close(agg, (sc.get_scores(0) + sc.get_scores(1)) / 2)
+    hot, warm, cold = sc.get_tier_assignments(0, 16, 6, 4)
+    assert hot.is_cuda and (hot.numel(), warm.numel(), cold.numel()) == (6, 4, 6)
+    assert {0, 1, 14, 15} <= set(hot.tolist())
