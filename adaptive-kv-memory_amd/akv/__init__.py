@@ -7,7 +7,7 @@ gfx950 kernels from libakv_hip.so.
 from .affine_quantizer import AffineQuantConfig, AffineQuantizer
 from .baselines import KIVICache, KIVIConfig, KIVIFusedCache, KIVIFusedConfig, create_baseline
 from .bitpack import pack, unpack, packed_bytes
-from .drop_in import AKVCache, _PRESETS, select_demote_indices
+from .drop_in import AKVCache, AKVLayer, _PRESETS, recommend_preset, select_demote_indices
 from .fused_attention import fused_int4_decode_attention, mixed_precision_decode_attention
 from .importance import ImportanceConfig, ImportanceScorer, ScoringStrategy
 from .packed_layout import PackedKVArena, PackedKVConfig, PagedKVCache
@@ -27,7 +27,7 @@ __version__ = "0.1.0"
 __all__ = [
     "AffineQuantConfig", "AffineQuantizer", "pack", "unpack", "packed_bytes",
     "KIVICache", "KIVIConfig", "KIVIFusedCache", "KIVIFusedConfig", "create_baseline",
-    "AKVCache", "_PRESETS", "select_demote_indices",
+    "AKVCache", "AKVLayer", "_PRESETS", "recommend_preset", "select_demote_indices",
     "fused_int4_decode_attention", "mixed_precision_decode_attention",
     "ImportanceConfig", "ImportanceScorer", "ScoringStrategy",
     "PackedKVArena", "PackedKVConfig", "PagedKVCache", "ProductionCache", "ProductionCacheConfig",

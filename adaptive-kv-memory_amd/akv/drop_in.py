@@ -564,6 +564,34 @@ class AKVLayer:
         self.keys, self.values = fk, fv
         return fk, fv
 
+    def crop(self, max_length: int):
+        """Keep positions 0 .. max_length-1 (the cache's ``crop``): hot tokens at or past
+        it leave the hot tier with their importance, warm ones leave the packed tier with
+        their proxy scores, and the length becomes max_length."""
+        if self._total_len <= max_length:
+            return
+        if self._hot_keys is not None:
+            keep = self._hot_positions < max_length
+            if not bool(keep.all()):
+                kd = keep.to(self._hot_keys.device)
+                self._hot_keys = self._hot_keys[:, :, kd]
+                self._hot_values = self._hot_values[:, :, kd]
+                self._hot_positions = self._hot_positions[keep]
+                if self._importance is not None and self._importance.shape[0] == keep.shape[0]:
+                    self._importance = self._importance[kd]
+        if self._warm is not None and self._warm_positions is not None:
+            wkeep = self._warm_positions < max_length
+            n_drop = int((~wkeep).sum())
+            if n_drop:
+                warm_len = int(wkeep.shape[0])
+                self._warm.keep(wkeep.to(self._warm.dev))
+                self._warm_positions = self._warm_positions[wkeep]
+                if self._proxy_score is not None and self._proxy_score.shape[0] == warm_len:
+                    self._proxy_score = self._proxy_score[wkeep.to(self._proxy_score.device)]
+                self._warm_bytes_packed = int(self._warm_bytes_packed * ((warm_len - n_drop) / warm_len))
+                self._warm_len -= n_drop
+        self._total_len = max_length
+
     def warm_view(self) -> tuple[Optional[torch.Tensor], Optional[torch.Tensor]]:
         """The dequantized warm tier in demotion order (the reference's working copy)."""
         if self._warm is None:
@@ -599,8 +627,10 @@ class AKVCache:
     """The drop-in cache (akv/drop_in.py:885-1200): preset resolution, protected
     layers, lazily created ``AKVLayer``s driven by ``update`` (the method an HF
     model calls per layer), and ``demote`` (the warm-tier hot path with 32-token
-    K blocks, for callers that manage the tiers themselves).  Subclassing HF's
-    ``DynamicCache`` is not part of this build."""
+    K blocks, for callers that manage the tiers themselves), with the reference's other
+    cache methods (length queries, iteration, the legacy tuple form, crop, the beam
+    helpers, reset, for_model, from_calibration).  Subclassing HF's ``DynamicCache`` is
+    not part of this build."""
 
     def __init__(self, preset: Optional[str] = None, warm_bits: Optional[int] = None,
                  warm_key_bits: Optional[int] = None, warm_value_bits: Optional[int] = None,
@@ -744,6 +774,102 @@ class AKVCache:
                 return (torch.cat([wk, layer._hot_keys], dim=2), torch.cat([wv, layer._hot_values], dim=2))
         return torch.tensor([]), torch.tensor([])
 
+    def __iter__(self):
+        for i in range(len(self.layers)):
+            yield self[i]
+
+    def to_legacy_cache(self):
+        """akv/drop_in.py:1203-1205: ((keys, values) per layer) as ``__getitem__`` gives them."""
+        return tuple(self[i] for i in range(len(self.layers)))
+
+    @classmethod
+    def from_legacy_cache(cls, past_key_values=None) -> "AKVCache":
+        """akv/drop_in.py:1273-1280: a default cache fed layer by layer through ``update``."""
+        cache = cls()
+        if past_key_values is not None:
+            for layer_idx, (k, v) in enumerate(past_key_values):
+                cache.update(k, v, layer_idx)
+        return cache
+
+    @property
+    def key_cache(self) -> list:
+        """akv/drop_in.py:1214-1221: each layer's keys as ``__getitem__`` gives them."""
+        return [self[i][0] for i in range(len(self.layers))]
+
+    @property
+    def value_cache(self) -> list:
+        """akv/drop_in.py:1223-1229."""
+        return [self[i][1] for i in range(len(self.layers))]
+
+    def crop(self, max_length: int):
+        """akv/drop_in.py:1231-1243 (speculative-decoding rewind): every layer keeps the
+        positions before ``max_length`` (a negative value counts back from the current
+        length, as transformers' caches take it).  The reference trims the hot tier from
+        its end, where the newest tokens are; a token past max_length that was already
+        demoted leaves the packed tier too here, so every layer's view stays whole."""
+        for layer in self.layers:
+            n = max_length if max_length >= 0 else max(0, layer.get_seq_length() + max_length)
+            layer.crop(n)
+
+    def batch_select_indices(self, indices: torch.Tensor) -> "AKVCache":
+        """akv/drop_in.py:1256-1265 (beam search): keep / reorder batch elements."""
+        self.reorder_cache(indices)
+        return self
+
+    def batch_repeat_interleave(self, repeats: int) -> "AKVCache":
+        """akv/drop_in.py:1245-1254 (beam expansion): each batch element ``repeats`` times
+        in a row, in both tiers."""
+        for layer in self.layers:
+            if layer._hot_keys is None:
+                continue
+            idx = torch.arange(layer._hot_keys.shape[0], device=layer._hot_keys.device).repeat_interleave(repeats)
+            layer._hot_keys = layer._hot_keys.index_select(0, idx)
+            layer._hot_values = layer._hot_values.index_select(0, idx)
+            if layer._warm is not None:
+                layer._warm.index_batch(idx)
+        return self
+
+    def reset(self):
+        """akv/drop_in.py:1267-1270: empty (every layer dropped, no tokens seen)."""
+        self.layers.clear()
+        self._seen_tokens = 0
+
+    @classmethod
+    def for_model(cls, model, **kwargs) -> "AKVCache":
+        """akv/drop_in.py:1012-1053: a cache sized from ``model.config``
+        (num_hidden_layers, or n_layer), the other arguments as given.  The reference
+        also applies per-family defaults from its model-adapter registry (preset and
+        protected layers) when the caller leaves them out; that registry is not part of
+        this build, so pass them explicitly."""
+        config = getattr(model, "config", None)
+        if config is None:
+            raise ValueError("model has no .config attribute")
+        n_layers = getattr(config, "num_hidden_layers", None) or getattr(config, "n_layer", None)
+        if n_layers is None:
+            raise ValueError("Could not find num_hidden_layers in model.config. Pass num_hidden_layers= explicitly.")
+        return cls(num_hidden_layers=n_layers, **kwargs)
+
+    @classmethod
+    def from_calibration(cls, calibration_path, **overrides) -> "AKVCache":
+        """akv/drop_in.py:1282-1315: a cache from a calibration report (JSON, the
+        reference's CalibrationReport fields): its protected layers and layer count, its
+        average width when within [2, 4] bits (else its preset), and its per-(layer, head)
+        widths; ``overrides`` win."""
+        import json
+        with open(calibration_path) as f:
+            rep = json.load(f)
+        kwargs = dict(protect_first=rep["recommended_protect_first"], protect_last=rep["recommended_protect_last"],
+                      num_hidden_layers=rep["num_layers"])
+        avg = float(rep["recommended_average_bits"])
+        if 2.0 <= avg <= 4.0:
+            kwargs["warm_bits"] = int(round(avg))
+        else:
+            kwargs["preset"] = rep["recommended_preset"]
+        kwargs.update(overrides)
+        cache = cls(**kwargs)
+        cache._calibration_per_head_bits = {int(k): list(v) for k, v in rep.get("per_head_bits", {}).items()}
+        return cache
+
     def demote(self, keys: torch.Tensor, values: torch.Tensor, importance: Optional[torch.Tensor],
                n_demote: int) -> tuple[WarmTier, torch.Tensor]:
         """Pick ``n_demote`` hot tokens per sequence (lowest importance, protected
@@ -758,3 +884,25 @@ class AKVCache:
         warm = quantize_kv(keys, values, self.warm_key_bits, self.warm_value_bits, self.block_t,
                            self.group_v, self.outlier_fraction, sel=idx)
         return warm, idx
+
+
+def recommend_preset(model, tokenizer=None, sample_text: Optional[str] = None) -> dict:
+    """akv/drop_in.py:1321-1366: a preset suggestion from ``model.config`` by a rough
+    size estimate, layers x kv-heads x head_dim^2 x 4 (the reference's heuristic and
+    its thresholds: above 5e9 balanced 3-bit, above 1e9 quality 4-bit with a 256-token
+    hot window, else quality 4-bit with 512 and two protected layers at each end)."""
+    config = getattr(model, "config", None)
+    if config is None:
+        return {"preset": "balanced", "reason": "No config found, using default"}
+    n_layers = getattr(config, "num_hidden_layers", 32)
+    n_heads = getattr(config, "num_key_value_heads", getattr(config, "num_attention_heads", 32))
+    head_dim = getattr(config, "head_dim", getattr(config, "hidden_size", 4096) // getattr(config, "num_attention_heads", 32))
+    est = n_layers * n_heads * head_dim * head_dim * 4
+    if est > 5e9:
+        return {"preset": "balanced", "warm_bits": 3, "hot_budget": 128, "protect_first": 2, "protect_last": 2,
+                "reason": f"Large model ({est / 1e9:.0f}B est.) \u2014 robust to 3-bit"}
+    if est > 1e9:
+        return {"preset": "quality", "warm_bits": 4, "hot_budget": 256, "protect_first": 1, "protect_last": 1,
+                "reason": f"Medium model ({est / 1e9:.1f}B est.) \u2014 use 4-bit for safety"}
+    return {"preset": "quality", "warm_bits": 4, "hot_budget": 512, "protect_first": 2, "protect_last": 2,
+            "reason": f"Small model ({est / 1e9:.1f}B est.) \u2014 protect more layers"}

@@ -114,3 +114,74 @@ def test_affine_quantizer_8bit_passthrough(packed):
         assert got["bits"] == 8 and got["codes"].shape[-1] == 128
     bits_equal(qz.dequantize_keys(qk), oaff.dequantize_keys(rk, packed=packed))
     bits_equal(qz.dequantize_values(qv), oaff.dequantize_values(rv, packed=packed))
+
+
+def _filled_cache(B=2, seed=31):
+    """A cache that has demoted: a 40-token prefill and three one-token steps at a hot
+    budget of 16 (promotion off, so the tiers only change by demotion)."""
+    import akv
+    cache = akv.AKVCache(warm_bits=3, hot_budget=16, enable_promotion=False, enable_promotion_proxy=False)
+    k, v = _kv((B, 2, 40, 128), seed)
+    views = [cache.update(to_dev(k), to_dev(v), 0)]
+    for step in range(3):
+        k1, v1 = _kv((B, 2, 1, 128), seed + 1 + step)
+        views.append(cache.update(to_dev(k1), to_dev(v1), 0))
+    return cache, views[-1]
+
+
+def test_crop_rewinds_both_tiers():
+    """crop(n) keeps positions 0..n-1: the next step's view starts with the old view's
+    first n rows (bit for bit) and holds n + 1 tokens; crop below the warm tier's positions
+    drops warm tokens too; a negative length counts back from the current one."""
+    announce("AKVCache.crop")
+    cache, view = _filled_cache()
+    fk, fv = view
+    assert cache.get_seq_length() == 43 and cache.layers[0]._warm.n > 0
+    cache.crop(38)
+    assert cache.get_seq_length() == 38
+    k1, v1 = _kv((2, 2, 1, 128), 99)
+    gk, gv = cache.update(to_dev(k1), to_dev(v1), 0)
+    assert gk.shape[2] == 39
+    assert torch.equal(gk[:, :, :38], fk[:, :, :38]) and torch.equal(gv[:, :, :38], fv[:, :, :38])
+    assert torch.equal(gk[:, :, 38:], to_dev(k1))
+    cache.crop(10)  # below positions already in the packed tier
+    layer = cache.layers[0]
+    assert cache.get_seq_length() == 10 and bool((layer._warm_positions < 10).all())
+    assert layer._warm.n == layer._warm_positions.numel() and layer._hot_keys.shape[2] + layer._warm.n == 10
+    gk, _ = cache.update(to_dev(k1), to_dev(v1), 0)
+    assert gk.shape[2] == 11 and torch.equal(gk[:, :, :10], fk[:, :, :10])
+    cache.crop(-3)
+    assert cache.get_seq_length() == 8
+
+
+def test_batch_helpers_iteration_and_legacy_form():
+    """batch_repeat_interleave / batch_select_indices reorder both tiers along the batch
+    (checked through the chronological view of the next step), __iter__, key_cache /
+    value_cache and to_legacy_cache give __getitem__'s tensors, from_legacy_cache feeds
+    update, reset empties."""
+    import akv
+    announce("AKVCache batch helpers / iteration / legacy form")
+    cache, view = _filled_cache()
+    ref = [t.clone() for t in cache[0]]
+    items = list(cache)
+    assert len(items) == 1 and all(torch.equal(a, b) for a, b in zip(items[0], ref))
+    assert torch.equal(cache.key_cache[0], ref[0]) and torch.equal(cache.value_cache[0], ref[1])
+    legacy = cache.to_legacy_cache()
+    assert torch.equal(legacy[0][0], ref[0])
+    cache.batch_repeat_interleave(2)
+    rep = cache[0]
+    assert rep[0].shape[0] == 4
+    for i, src in enumerate((0, 0, 1, 1)):
+        assert torch.equal(rep[0][i], ref[0][src]) and torch.equal(rep[1][i], ref[1][src])
+    cache.batch_select_indices(torch.tensor([3, 0], device="cuda"))
+    sel = cache[0]
+    assert torch.equal(sel[0][0], ref[0][1]) and torch.equal(sel[0][1], ref[0][0])
+    cache.crop(42)  # one hot token fewer, so the next step demotes nothing and the old rows stay as they were
+    k1, v1 = _kv((2, 2, 1, 128), 77)
+    gk, _ = cache.update(to_dev(k1), to_dev(v1), 0)
+    assert torch.equal(gk[0, :, :42], view[0][1, :, :42]) and torch.equal(gk[1, :, :42], view[0][0, :, :42])
+    k, v = _kv((1, 2, 5, 128), 5)
+    c2 = akv.AKVCache.from_legacy_cache(((to_dev(k), to_dev(v)), (to_dev(k), to_dev(v))))
+    assert len(c2) == 2 and c2.get_seq_length(1) == 5 and torch.equal(c2[1][0], to_dev(k))
+    c2.reset()
+    assert len(c2) == 0

@@ -115,3 +115,61 @@ def test_cache_length_queries_and_arena_config():
     for bits, pf in ((2, 4), (4, 2), (8, 1)):
         c = PackedKVConfig(head_dim=128, bits=bits, group_size=48, device="cpu")
         assert (c.pack_factor, c.packed_dim, c.num_groups) == (pf, 128 // pf, 3)
+
+
+class _Cfg:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+class _Model:
+    def __init__(self, **kw):
+        self.config = _Cfg(**kw)
+
+
+def test_recommend_preset_thresholds():
+    """recommend_preset (akv/drop_in.py:1321-1366): layers x kv-heads x head_dim^2 x 4
+    against 5e9 and 1e9 (so common models land in the last branch: Qwen2.5-1.5B is 3.7e6)."""
+    import akv
+    assert akv.recommend_preset(object())["preset"] == "balanced"
+    big = akv.recommend_preset(_Model(num_hidden_layers=100, num_key_value_heads=128, head_dim=512))  # 1.3e10
+    assert (big["preset"], big["warm_bits"], big["hot_budget"], big["protect_first"]) == ("balanced", 3, 128, 2)
+    mid = akv.recommend_preset(_Model(num_hidden_layers=64, num_key_value_heads=64, head_dim=256))  # 1.07e9
+    assert (mid["preset"], mid["warm_bits"], mid["hot_budget"], mid["protect_last"]) == ("quality", 4, 256, 1)
+    small = akv.recommend_preset(_Model(num_hidden_layers=28, num_key_value_heads=2, hidden_size=1536,
+                                        num_attention_heads=12))  # head_dim 128 from hidden / heads
+    assert (small["preset"], small["hot_budget"], small["protect_first"]) == ("quality", 512, 2)
+
+
+def test_for_model_and_from_calibration(tmp_path):
+    import json
+    import akv
+    c = akv.AKVCache.for_model(_Model(num_hidden_layers=12), preset="compact", protect_last=2)
+    assert c.num_hidden_layers == 12 and c._is_protected(11) and c._is_protected(10) and not c._is_protected(9)
+    assert akv.AKVCache.for_model(_Model(n_layer=6)).num_hidden_layers == 6
+    with pytest.raises(ValueError, match="no .config"):
+        akv.AKVCache.for_model(object())
+    with pytest.raises(ValueError, match="num_hidden_layers"):
+        akv.AKVCache.for_model(_Model(hidden_size=64))
+    rep = {"model_name": "m", "model_type": "llama", "num_layers": 8, "num_kv_heads": 2, "head_dim": 128,
+           "kv_outlier_ratio": 3.0, "attention_entropy_mean": 1.0, "attention_sink_strength": 0.1,
+           "recommended_preset": "quality", "recommended_protect_first": 1, "recommended_protect_last": 1,
+           "recommended_average_bits": 2.6, "per_head_bits": {"0": [2, 4], "3": [3, 3]}, "sensitivities": []}
+    path = tmp_path / "calib.json"
+    path.write_text(json.dumps(rep))
+    c = akv.AKVCache.from_calibration(str(path))
+    assert c.warm_bits == 3 and c.num_hidden_layers == 8 and c._is_protected(0) and c._is_protected(7)
+    assert c._calibration_per_head_bits == {0: [2, 4], 3: [3, 3]}
+    rep["recommended_average_bits"] = 6.0
+    path.write_text(json.dumps(rep))
+    c = akv.AKVCache.from_calibration(str(path), protect_first=0)
+    assert c.preset == "quality" and c.warm_bits == 4 and not c._is_protected(0)
+
+
+def test_empty_cache_views_and_reset():
+    import akv
+    c = akv.AKVCache()
+    assert list(c) == [] and c.to_legacy_cache() == () and c.key_cache == [] and c.value_cache == []
+    c._seen_tokens = 5
+    c.reset()
+    assert len(c) == 0 and c.seen_tokens == 0
