@@ -383,9 +383,10 @@ class AKVLayer:
 
     def __init__(self, warm_bits: int = 3, hot_budget: int = 128, group_size: int = 64, protect: bool = False,
                  enable_promotion: bool = True, promotion_threshold: float = 0.05,
+                 per_head_bits: Optional[list] = None,
                  enable_promotion_proxy: bool = True, proxy_decay: float = 0.7, adaptive_hot_frac: float = 0.0,
                  warm_key_bits: Optional[int] = None, warm_value_bits: Optional[int] = None,
-                 outlier_fraction: float = 0.0, per_head_bits: Optional[list] = None):
+                 outlier_fraction: float = 0.0):
         self.warm_bits = warm_bits
         self.hot_budget = hot_budget
         self.group_size = group_size

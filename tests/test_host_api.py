@@ -173,3 +173,14 @@ def test_empty_cache_views_and_reset():
     c._seen_tokens = 5
     c.reset()
     assert len(c) == 0 and c.seen_tokens == 0
+
+
+def test_layer_constructor_parameter_order():
+    """AKVLayer's parameters in the reference's order (akv/drop_in.py:162-177), so
+    positional calls bind as they do there."""
+    import inspect
+    import akv
+    params = list(inspect.signature(akv.AKVLayer.__init__).parameters)[1:]
+    assert params == ["warm_bits", "hot_budget", "group_size", "protect", "enable_promotion",
+                      "promotion_threshold", "per_head_bits", "enable_promotion_proxy", "proxy_decay",
+                      "adaptive_hot_frac", "warm_key_bits", "warm_value_bits", "outlier_fraction"]
