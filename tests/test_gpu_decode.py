@@ -205,6 +205,34 @@ def test_split_counts_agree():
         assert_close_attn(_run(q, kh, vh, w, False, num_splits=ns), ref)
 
 
+@pytest.fixture(scope="module")
+def long_case():
+    return _case(1, 8, 2, 128, 256, 40960, 2, 2, seed=13)
+
+
+@pytest.mark.parametrize("weights", [True, False])
+def test_long_context_many_splits_importance(long_case, weights):
+    """One sequence, 2 kv heads, 40k warm + 256 hot tokens: the planner spreads the two
+    (batch, kv-head) pairs over 128 splits each, past what the in-kernel merge takes, so
+    the separate merge kernel finishes the output, the weights and the importance EMA
+    (with the weights returned, or from the logit stash without them)."""
+    announce(f"decode 40k tokens, automatic splits, weights={weights}")
+    q, kh, vh, w, kd, vd = long_case
+    N = kh.shape[2] + w["N"]
+    s0 = np.random.default_rng(5).random(N + 11).astype(np.float32)
+    sc = to_dev(s0)
+    res = _run(q, kh, vh, w, False, scores=sc, decay=0.95, return_weights=weights)
+    ref, ref_attn = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False)
+    out = res[0] if weights else res
+    assert_close_attn(out, ref)
+    if weights:
+        a = res[1].cpu().numpy()
+        np.testing.assert_allclose(a, ref_attn, atol=2e-6, rtol=1e-4)
+        np.testing.assert_allclose(a.sum(-1), 1.0, atol=1e-5)
+    np.testing.assert_allclose(sc.cpu().numpy(), oimp.fused_importance_update(ref_attn, s0, 0.95),
+                               rtol=1e-5, atol=1e-6)
+
+
 def test_full_size_qwen_32k_slice():
     """One layer of the 32k workload at full size; the oracle checks one batch element."""
     import akv
