@@ -173,6 +173,43 @@ def test_per_head_bits_match_oracle(of):
     _same(fk.flip(0), ok, "view after reorder_cache([1, 0]) with per-head widths")
 
 
+def test_calibrated_widths_reach_their_layers(tmp_path):
+    """tests/test_per_head_bits.py restated: a calibration report's widths reach the
+    layers it names, one packed tier per distinct width; an uncalibrated layer keeps
+    the global width; a layer whose head count differs from its calibration falls back
+    to the global width and still demotes."""
+    import json
+    from akv.drop_in import AKVCache, AKVLayer, _HeadBitsTier
+    announce("per-head widths from a calibration report")
+    rep = {"model_name": "x", "model_type": "llama", "num_layers": 4, "num_kv_heads": 2, "head_dim": 64,
+           "recommended_preset": "balanced", "recommended_protect_first": 0, "recommended_protect_last": 0,
+           "recommended_average_bits": 3.0, "per_head_bits": {"0": [2, 3], "1": [4, 4]}}
+    path = tmp_path / "calib.json"
+    path.write_text(json.dumps(rep))
+    cache = AKVCache.from_calibration(str(path), hot_budget=2, enable_promotion=False)
+    g = torch.Generator().manual_seed(41)
+    k = torch.randn(1, 2, 6, 64, generator=g).half().cuda()
+    v = torch.randn(1, 2, 6, 64, generator=g).half().cuda()
+    for li in range(3):
+        cache.update(k, v, li)
+    assert cache.layers[0].per_head_bits == [2, 3] and cache.layers[1].per_head_bits == [4, 4]
+    assert cache.layers[2].per_head_bits is None
+    assert [grp[0] for grp in cache.layers[0]._warm.groups] == [2, 3]
+    assert [grp[0] for grp in cache.layers[1]._warm.groups] == [4]
+    assert not isinstance(cache.layers[2]._warm, _HeadBitsTier)
+    for li in range(3):
+        layer = cache.layers[li]
+        assert layer._warm_len == 4 and layer.get_seq_length() == 6
+    # one more token through the per-width tiers: the view holds all seven
+    fk0, _ = cache.layers[0].update(k[:, :, :1], v[:, :, :1])
+    assert fk0.shape == (1, 2, 7, 64) and torch.isfinite(fk0).all()
+
+    layer = AKVLayer(warm_bits=3, hot_budget=2, enable_promotion=False, per_head_bits=[2, 3, 4, 2])
+    fk, fv = layer.update(k[:, :, :4], v[:, :, :4])
+    assert layer._warm_len == 2 and not isinstance(layer._warm, _HeadBitsTier)
+    assert fk.shape == fv.shape == (1, 2, 4, 64)
+
+
 def test_promotion_from_attention_weights():
     """Warm columns of the attention weights above the threshold (6 of them, cap 4):
     the top 4 return to the front of the hot tier with their float16 values."""
