@@ -34,6 +34,12 @@ __device__ __forceinline__ u4 rsrc4(const void *base, uint32_t bytes) {
 // M0 is written several instructions before the load that reads it.  The
 // loads are non-temporal (each byte is read once; measured 0.5 us per layer
 // faster at the 32k decode workload than the default policy).
+// Inline asm is opaque to the compiler's hazard checks, so each block brings the
+// wait states its first load needs: a VMEM instruction may read an SGPR only 5
+// wait states after a VALU wrote it, and the compiler keeps some buffer
+// descriptors spilled in VGPR lanes and reloads them with v_readlane_b32 (a VALU
+// write) right before a block.  Here the four SALU instructions and the s_nop 0
+// make 5; the block of dma_lean opens with two and an s_nop 2.
 __device__ __forceinline__ void dma16(u4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff, uint64_t mask) {
     uint64_t saved;
     uint32_t saved_m0;
@@ -65,7 +71,7 @@ template <int BYTES>
 __host__ __device__ constexpr int dma_count() {
     return BYTES / 1024 + (BYTES % 1024) / 256;
 }
-#define AKV_DMA_HEAD "s_mov_b32 %[sm0], m0\n\ts_mov_b32 m0, %[lds]\n\ts_nop 0\n\t"
+#define AKV_DMA_HEAD "s_mov_b32 %[sm0], m0\n\ts_mov_b32 m0, %[lds]\n\ts_nop 2\n\t"
 #define AKV_DMA_X4(off) "buffer_load_dwordx4 %[v16], %[rsrc], %[soff] offen offset:" #off " nt lds\n\t"
 #define AKV_DMA_X1(off) "buffer_load_dword %[v4], %[rsrc], %[soff] offen offset:" #off " nt lds\n\t"
 #define AKV_DMA_TAIL "s_mov_b32 m0, %[sm0]"
@@ -259,17 +265,27 @@ struct Soft {
 // row's tile max passes the bound iff one of its four lanes' maxima does.  On
 // the rare update the four lanes of a row agree on the new max through two
 // shuffles.  Returns the fp16 P^T operand (x 2^7).
-// max of three (IEEE maxNum, as fmaxf).  fmaxf over values the compiler cannot
-// prove canonical (MFMA results) costs an extra v_max per operand to quiet
-// signalling NaNs; the scores never hold one, so this takes them as they are.
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-    float r;
-    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-    return r;
+// Maximum of a tile's scores straight from the MFMAs, as IEEE maximum (nested, so
+// one or two v_maximum3_f32).  fmaxf over values the compiler cannot prove
+// canonical (MFMA results) costs an extra v_max per operand to quiet signalling
+// NaNs; maximum needs none, and the scores never hold a NaN, so both give the same
+// max.  It must be an operation the compiler sees: a VALU may read the result of
+// v_mfma_f32_16x16x32_f16 only 8 wait states after it issues, and the compiler
+// inserts those only before instructions it knows.  An inline-asm v_max3_f32 here
+// read stale registers once nothing else separated it from the last MFMA.
+__device__ __forceinline__ float mfma_max4(f4 s) {
+    return __builtin_elementwise_maximum(
+        __builtin_elementwise_maximum(__builtin_elementwise_maximum(s[0], s[1]), s[2]), s[3]);
+}
+__device__ __forceinline__ float mfma_max8(f4 a, f4 b) {
+    const float m0 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a[0], a[1]), a[2]);
+    const float m1 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(a[3], b[0]), b[1]);
+    const float m2 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(b[2], b[3]), b[3]);
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(m0, m1), m2);
 }
 
 __device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
-    const float t = vmax3(vmax3(s[0], s[1], s[2]), s[3], s[3]) * sl2;
+    const float t = mfma_max4(s) * sl2;
     if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
         const float tm2 = wmax16(t);
         const float mn = fmaxf(st.m2, tm2);
@@ -292,7 +308,7 @@ __device__ __forceinline__ h4 softmax16(Soft &st, f4 s, float sl2) {
 // fp16 P^T operand of a 16x16x32 MFMA whose K index 8*grp + j is token
 // 4*grp + j of half 0 (j < 4) or of half 1 (j >= 4).
 __device__ __forceinline__ h8 softmax32(Soft &st, f4 s0, f4 s1, float sl2) {
-    const float t = vmax3(vmax3(s0[0], s0[1], s0[2]), vmax3(s0[3], s1[0], s1[1]), vmax3(s1[2], s1[3], s1[3])) * sl2;
+    const float t = mfma_max8(s0, s1) * sl2;
     if (__builtin_amdgcn_ballot_w64(t > st.m2 + kThreshF)) {
         const float tm2 = wmax16(t);
         const float mn = fmaxf(st.m2, tm2);
