@@ -103,6 +103,12 @@ def test_adaptive_budget_and_protected_layers():
     assert cache.layers[1]._hot_keys.shape[2] == max(32, int(0.25 * 232))
     rep = cache.memory_report()
     assert rep["num_layers"] == 3 and rep["seq_length"] == 232 and rep["savings_ratio"] > 1.0
+    # the aggregator's keys (tests/test_memory_alignment.py:140-165)
+    stats = cache.memory_usage()
+    assert set(stats) == {"hot_bytes", "warm_bytes", "warm_bytes_live", "warm_bytes_packed", "warm_bytes_formula",
+                          "total_bytes", "fp16_equivalent_bytes", "savings_ratio", "num_layers"}
+    assert 0 < stats["warm_bytes"] == stats["warm_bytes_packed"] <= stats["warm_bytes_live"]
+    assert stats["total_bytes"] == stats["hot_bytes"] + stats["warm_bytes_packed"]
 
 
 def test_getitem_and_reorder_cache():
