@@ -2,14 +2,17 @@
 
 The compiler inserts the wait states a hardware hazard needs (``s_nop``) only
 between instructions it generated itself; an inline-asm block is opaque to that
-check, so the block has to carry its own.  Two hazards can reach one here:
+check, so the block has to carry its own.  Three hazards can reach one here:
 
 * a VMEM instruction (``buffer_``/``global_``/``flat_``) may read an SGPR only 5
   wait states after a VALU instruction wrote it -- the compiler keeps buffer
   descriptors spilled in VGPR lanes and reloads them with ``v_readlane_b32`` right
   before a block;
 * a VALU instruction may read the result of ``v_mfma_f32_16x16x32_f16`` only 8
-  wait states after the MFMA issued.
+  wait states after the MFMA issued;
+* a VALU instruction may read the result of a transcendental VALU instruction
+  (``v_exp``, ``v_log``, ``v_rcp``, ``v_rsq``, ``v_sqrt``, ``v_sin``, ``v_cos``) only 1
+  wait state after it.
 
 For every VMEM or VALU instruction inside an ``;;#ASMSTART`` / ``;;#ASMEND`` block,
 ``check`` walks back over every control-flow path (fall-through and each branch
@@ -26,6 +29,8 @@ import sys
 
 VALU_SGPR_WAIT = 5   # VALU writes an SGPR -> VMEM reads it
 MFMA_VALU_WAIT = 8   # v_mfma_f32_16x16x32_f16 writes a VGPR -> VALU reads it
+TRANS_VALU_WAIT = 1  # a transcendental VALU op writes a VGPR -> VALU reads it
+_TRANS = re.compile(r"^v_(exp|log|rcp|rsq|sqrt|sin|cos)_")
 _HORIZON = max(VALU_SGPR_WAIT, MFMA_VALU_WAIT)
 
 
@@ -83,6 +88,8 @@ def check(asm_text: str) -> tuple:
                 hits.append(f"VALU writes an SGPR {ws} wait states before: {t}")
             if need_v and op.startswith("v_mfma") and ws < MFMA_VALU_WAIT and _regs(dst, "v") & need_v:
                 hits.append(f"MFMA writes a VGPR {ws} wait states before: {t}")
+            if need_v and _TRANS.match(op) and ws < TRANS_VALU_WAIT and _regs(dst, "v") & need_v:
+                hits.append(f"a transcendental op writes a VGPR {ws} wait states before: {t}")
             ws += int(args.strip()) + 1 if op == "s_nop" else 1
             kk -= 1
 

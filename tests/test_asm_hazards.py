@@ -2,9 +2,9 @@
 
 The compiler guards hardware hazards only between instructions it generated;
 ``csrc/asm_hazards.py`` checks every inline-asm VMEM / VALU instruction of the
-gfx950 assembly of this build (``make asm``) against the two hazards that can reach
-one here (a VALU-written SGPR read by a buffer load within 5 wait states, an MFMA
-result read by a VALU within 8).  The checker itself is pinned on planted cases."""
+gfx950 assembly of this build (``make asm``) against the hazards that can reach one
+here (a VALU-written SGPR read by a buffer load within 5 wait states, an MFMA result
+read by a VALU within 8, a transcendental result read by a VALU within 1).  The checker itself is pinned on planted cases."""
 import importlib.util
 import os
 import shutil
@@ -66,6 +66,12 @@ def test_checker_finds_planted_hazards():
     assert n == 1 and len(hz) == 2 and all("SGPR" in h for h in hz)
     # s_nop 2 makes 5 and 6
     n, hz = chk.check(_READLANE_THEN_DMA.format(nop=2))
+    assert n == 1 and hz == []
+    # a reciprocal read by the next (asm) instruction, then with one instruction between
+    rcp = "k:\n\tv_rcp_f32_e32 v3, v2\n{mid}\t;;#ASMSTART\n\tv_fma_mixlo_f16 v5, v4, v3, 0\n\t;;#ASMEND\n"
+    n, hz = chk.check(rcp.format(mid=""))
+    assert n == 1 and len(hz) == 1 and "transcendental" in hz[0]
+    n, hz = chk.check(rcp.format(mid="\tv_mov_b32_e32 v6, v7\n"))
     assert n == 1 and hz == []
 
 
