@@ -45,7 +45,7 @@ struct DecodeParams {
     uint64_t *split_ctr;          // fast kernel: arrival counts per (b, kv-head, row chunk), a byte per XCD; null = merge
                                   // in decode_reduce_kernel / finish_kernel
     float *stash;                 // [B][Hq][M][N] raw logits q.k (or null); x * scale_log2 is the log2 domain
-    float *rowstats;              // [B*Hq*M][2] (M, L)
+    float *rowstats;              // [B*Hq*M][2] (M, 1 / L): the reciprocal once per row
     _Float16 *out;                // [B][Hq][M][D]
     int out_bf16;                 // reduce only: write bf16 (chunked prefill with bf16 queries)
     float *attn_out;              // normalised weights (or null)

@@ -786,7 +786,7 @@ __device__ __forceinline__ void merge_split_row(const DecodeParams &p, int bhc, 
         }
         if (tid == 0 && p.rowstats) {
             p.rowstats[2 * row] = M;
-            p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
+            p.rowstats[2 * row + 1] = 1.0f / (L * (1.0f / 128.0f));  // 1 / L, the 2^7 probability scale undone
         }
     }
 }
@@ -839,7 +839,7 @@ __global__ __launch_bounds__(256) void reduce_few_kernel(const DecodeParams p) {
     }
     if (q == 0 && p.rowstats) {
         p.rowstats[2 * row] = M;
-        p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
+        p.rowstats[2 * row + 1] = 1.0f / (L * (1.0f / 128.0f));  // 1 / L, the 2^7 probability scale undone
     }
 }
 
@@ -863,7 +863,7 @@ __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodePar
     float imp[4] = {0.f, 0.f, 0.f, 0.f};
     const int64_t N = p.N;
     for (int64_t r = rl; r < rows; r += 16) {
-        const float M = p.rowstats[2 * r], inv = 1.0f / p.rowstats[2 * r + 1];
+        const float M = p.rowstats[2 * r], inv = p.rowstats[2 * r + 1];
         float *srow = p.stash + r * N;
         float x[4];
 #pragma unroll
@@ -906,10 +906,11 @@ __global__ __launch_bounds__(256) void weights_importance_kernel(const DecodePar
 // token quads per workgroup (4 tokens each): 8 (32 tokens, 32 row lanes) measured
 // fastest at the 32k workload (16: +0.6 us per layer, 4: +2.5 us, 32: +13 us)
 constexpr int kWsQuads = AKV_WS_QUADS;
-template <bool VEC>
+// RB: rows per thread and batch of loads, chosen by the host so that one batch covers
+// every row when there are few (the 32k Qwen layer: 96 rows, 3 per thread), else 8.
+template <bool VEC, int RB>
 __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p) {
     constexpr int NQ = kWsQuads, TPW = 4 * NQ, NRL = 256 / NQ;  // tokens per workgroup, row lanes
-    constexpr int RB = NRL >= 16 ? 8 : 12;                      // rows per batch of loads
     __shared__ float red[NRL][TPW + 1];
     const int tid = threadIdx.x, q = tid % NQ, rl = tid / NQ;
     const int64_t rows = (int64_t)p.B * p.Hq * p.M, N = p.N;
@@ -930,7 +931,7 @@ __global__ __launch_bounds__(256) void weights_stats_kernel(const DecodeParams p
             x[j] = (f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
             if (r < rows) {
                 M[j] = p.rowstats[2 * r];
-                W[j] = 1.0f / p.rowstats[2 * r + 1];
+                W[j] = p.rowstats[2 * r + 1];
                 const float *src = p.stash + r * N + n0;
                 if (VEC && n0 + 3 < N) {
                     x[j] = __builtin_nontemporal_load((const f4 *)src);  // read once
@@ -1014,7 +1015,7 @@ __global__ __launch_bounds__(256) void finish_kernel(const DecodeParams p) {
     if (p.split_ctr) {
         for (int r = tid; r < rows; r += 256) {
             rM[r] = p.rowstats[2 * r];
-            rW[r] = 1.0f / p.rowstats[2 * r + 1];
+            rW[r] = p.rowstats[2 * r + 1];
         }
     }
     for (int r = tid; r < rows && !p.split_ctr; r += 256) {
@@ -1180,8 +1181,19 @@ hipError_t decode_launch(const DecodeParams &p, int kb, int vb, int wk, const in
         // the split kernel merged its splits and wrote the row statistics
         const int64_t nmax = p.N > p.n_scores ? p.N : p.n_scores;
         const dim3 g((unsigned)((nmax + 4 * kWsQuads - 1) / (4 * kWsQuads)));
-        if (p.N % 4 == 0) hipLaunchKernelGGL(weights_stats_kernel<true>, g, dim3(256), 0, s, p);
-        else hipLaunchKernelGGL(weights_stats_kernel<false>, g, dim3(256), 0, s, p);
+        constexpr int NRL = 256 / kWsQuads;
+        const int64_t per = (rows + NRL - 1) / NRL;  // rows per thread
+#define AKV_WS(RB)                                                                                 \
+    do {                                                                                           \
+        if (p.N % 4 == 0) hipLaunchKernelGGL((weights_stats_kernel<true, RB>), g, dim3(256), 0, s, p); \
+        else hipLaunchKernelGGL((weights_stats_kernel<false, RB>), g, dim3(256), 0, s, p);        \
+    } while (0)
+        if (per <= 1) AKV_WS(1);
+        else if (per <= 2) AKV_WS(2);
+        else if (per <= 3) AKV_WS(3);
+        else if (per <= 4) AKV_WS(4);
+        else AKV_WS(8);
+#undef AKV_WS
         return hipGetLastError();
     }
     if (p.stash && rows <= kFinishRows) {

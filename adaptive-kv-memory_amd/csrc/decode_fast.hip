@@ -1147,7 +1147,7 @@ void decode_fast_kernel(const DecodeParams p) {
         if (tid == 0) AKV_TL(6, AKV_TL_NOW());
         if (c4 == 0 && p.rowstats) {
             p.rowstats[2 * row] = M;
-            p.rowstats[2 * row + 1] = L * (1.0f / 128.0f);  // undo the 2^7 probability scale
+            p.rowstats[2 * row + 1] = 1.0f / (L * (1.0f / 128.0f));  // 1 / L, the 2^7 probability scale undone
         }
     }
     AKV_TL_FLUSH();
