@@ -205,6 +205,28 @@ def test_split_counts_agree():
         assert_close_attn(_run(q, kh, vh, w, False, num_splits=ns), ref)
 
 
+@pytest.mark.parametrize("B,Hq,M", [(4, 12, 1), (5, 12, 2), (8, 12, 2), (8, 10, 4)])
+def test_importance_rows_per_thread(B, Hq, M):
+    """The weights / importance pass after the in-kernel merge takes 1, 2, 3, 4 or 8 rows
+    per thread (B * Hq * M rows over 32 row lanes): 48, 120, 192 and 320 rows run the 2-,
+    4- and 8-row instantiations (320 in two batches of loads), checked with the weights
+    returned and with the importance alone."""
+    announce(f"decode importance rows per thread: B={B} Hq={Hq} M={M}")
+    q, kh, vh, w, kd, vd = _case(B, Hq, 2, 128, 64, 448, 3, 3, M=M, seed=14)
+    N = kh.shape[2] + w["N"]
+    s0 = np.random.default_rng(6).random(N + 3).astype(np.float32)
+    ref, ref_attn = oatt.mixed_attention_fp32(q, kh, vh, kd, vd, hot_first=False)
+    ref_sc = oimp.fused_importance_update(ref_attn, s0, 0.9)
+    sc = to_dev(s0)
+    out, attn = _run(q, kh, vh, w, False, scores=sc, decay=0.9, return_weights=True)
+    assert_close_attn(out, ref)
+    np.testing.assert_allclose(attn.cpu().numpy(), ref_attn, atol=2e-6, rtol=1e-4)
+    np.testing.assert_allclose(sc.cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-6)
+    sc2 = to_dev(s0)
+    _run(q, kh, vh, w, False, scores=sc2, decay=0.9)
+    np.testing.assert_allclose(sc2.cpu().numpy(), ref_sc, rtol=1e-5, atol=1e-6)
+
+
 @pytest.fixture(scope="module")
 def long_case():
     return _case(1, 8, 2, 128, 256, 40960, 2, 2, seed=13)
